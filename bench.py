@@ -1,0 +1,260 @@
+#!/usr/bin/env python3
+"""TurboQuant hot-path benchmark on one MI355X.
+
+Workload: Llama-3.1-8B KV shape -- batch 8, 32 query heads,
+8 KV heads, head_dim 128, context 32768 -- with 4-bit Q_prod keys (3-bit MSE +
+1-bit QJL) and 4-bit Q_mse values, 32 independently seeded layers of
+synthetic K/V (iid N(0,1) directions, lognormal(ln 20, 0.3) norms) quantized
+on the GPU by the prefill quantizer.
+
+A "step" is one decode step: the fused decode attention over all 32 layers
+(one query token per sequence, every layer a different packed cache, so the
+9 GB working set defeats the 256 MB Infinity Cache).  ``value`` is the
+whole-job packed-KV read rate in GB/s over the timed steps (inputs resident
+in HBM).  The prefill quantizer is timed separately and reported beside it.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "tq-local_amd", ROOT):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+VALU_FP32_PEAK_TFLOPS = 157.3
+
+
+def packed_bytes_per_token_head(dim: int, bits: int, qjl: bool) -> int:
+    kb = bits - 1 if qjl else bits
+    b = math.ceil(dim * kb / 8) + 2 + math.ceil(dim * bits / 8) + 2
+    if qjl:
+        b += dim // 8 + 2
+    return b
+
+
+def cpu_baseline(bits: int = 4) -> dict:
+    """BASELINE config 1 (B=1, Hq=32, Hkv=8, N=4096) through the torch restatement of
+    the reference's CPU path: encode (K Q_prod + V Q_mse) and one decode-attention step."""
+    import numpy as np
+    import torch
+
+    from oracle import torch_ref
+    from turboquant.quantization.turboquant_mse import codebook_f32, generate_qjl_matrix, random_rotation_matrix
+    from turboquant.runtime.synthetic import kv_bf16, query_bf16
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    B, Hq, Hkv, N, D = 1, 32, 8, 4096, 128
+    ck, bk = codebook_f32(D, bits - 1)
+    cv, bv = codebook_f32(D, bits)
+    params = {
+        "Rk": torch.from_numpy(random_rotation_matrix(D, 1)), "Ck": torch.from_numpy(ck), "Bk": torch.from_numpy(bk),
+        "Rv": torch.from_numpy(random_rotation_matrix(D, 0)), "Cv": torch.from_numpy(cv), "Bv": torch.from_numpy(bv),
+        "S": generate_qjl_matrix(D, 31337),
+    }
+    k = kv_bf16((B, Hkv, N, D), seed=11, device="cpu")
+    v = kv_bf16((B, Hkv, N, D), seed=12, device="cpu")
+    q = query_bf16(B, Hq, D, seed=13, device="cpu").unsqueeze(2)
+
+    def timed(fn, reps=5, warm=2):
+        for _ in range(warm):
+            fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    layer = torch_ref.encode_layer(k, v, params, True, bits)
+    t_enc = timed(lambda: torch_ref.encode_layer(k, v, params, True, bits))
+    t_att = timed(lambda: torch_ref.chunked_attention(q, layer, Hq // Hkv))
+    nbytes = B * Hkv * N * packed_bytes_per_token_head(D, bits, True)
+    cpu_model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / t_att / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config 1 (B=1, Hq=32, Hkv=8, D=128, N=4096, 4-bit Q_prod) through oracle/torch_ref.py "
+                   f"(reference CPU path): decode attention {t_att * 1e6:.0f} us/layer "
+                   f"({nbytes} packed bytes), encode K+V {t_enc * 1e3:.1f} ms; median of 5 after 2 warmups"),
+        "attention_us_per_layer": round(t_att * 1e6, 1),
+        "encode_ms_per_layer": round(t_enc * 1e3, 2),
+        "cpu_model": cpu_model,
+        "affinity_cpus": threads,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--q-heads", type=int, default=32)
+    ap.add_argument("--kv-heads", type=int, default=8)
+    ap.add_argument("--bits", type=int, default=4)
+    ap.add_argument("--no-qjl", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the TurboQuant decode path is single-GPU "
+              "(every configuration fits one MI355X); multi-GPU sharding is design-only.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from turboquant.runtime import kernels as K
+    from turboquant.runtime.params import layer_codecs
+    from turboquant.runtime.synthetic import kv_bf16, query_bf16
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, N, D, bits = args.batch, args.q_heads, args.kv_heads, args.context, 128, args.bits
+    qjl = not args.no_qjl
+    lc = layer_codecs(D, bits, 0, qjl, dev)
+    per_tok = packed_bytes_per_token_head(D, bits, qjl)
+    layer_bytes = B * Hkv * N * per_tok
+
+    # ------------------------------------------------ prefill quantize all layers
+    layers, queries, q_ms = [], [], []
+    for li in range(args.layers):
+        k = kv_bf16((B, Hkv, N, D), seed=1000 + 2 * li, device=dev)
+        v = kv_bf16((B, Hkv, N, D), seed=1001 + 2 * li, device=dev)
+        L = {
+            "k_codes": torch.empty(B, Hkv, N, K.row_bytes(D, lc.key_bits), dtype=torch.uint8, device=dev),
+            "k_norms": torch.empty(B, Hkv, N, dtype=torch.float16, device=dev),
+            "v_codes": torch.empty(B, Hkv, N, K.row_bytes(D, bits), dtype=torch.uint8, device=dev),
+            "v_norms": torch.empty(B, Hkv, N, dtype=torch.float16, device=dev),
+            "k_signs": torch.empty(B, Hkv, N, D // 8, dtype=torch.uint8, device=dev) if qjl else None,
+            "k_rnorms": torch.empty(B, Hkv, N, dtype=torch.float16, device=dev) if qjl else None,
+        }
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        if qjl:
+            K.quantize_prod(k, lc.key, lc.qjl, L["k_codes"], L["k_norms"], L["k_signs"], L["k_rnorms"])
+        else:
+            K.quantize_mse(k, lc.key, L["k_codes"], L["k_norms"])
+        K.quantize_mse(v, lc.value, L["v_codes"], L["v_norms"])
+        e1.record()
+        torch.cuda.synchronize()
+        q_ms.append(e0.elapsed_time(e1))
+        del k, v
+        layers.append(L)
+        queries.append(query_bf16(B, Hq, D, seed=5000 + li, device=dev))
+    print(f"[bench] quantized {args.layers} layers: {statistics.median(q_ms):.3f} ms/layer (median)",
+          file=sys.stderr, flush=True)
+
+    def attn(li):
+        L = layers[li]
+        return K.decode_attention(queries[li], n_tokens=N, key=lc.key, value=lc.value, qjl=lc.qjl, **L)
+
+    for _ in range(args.warmup):
+        for li in range(args.layers):
+            attn(li)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps * args.layers)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps * args.layers)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = 0
+    for _ in range(args.steps):
+        for li in range(args.layers):
+            starts[i].record(stream)
+            attn(li)
+            ends[i].record(stream)
+            i += 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    call_us = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
+    avg_us = statistics.fmean(call_us)
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = layer_bytes * args.layers * args.steps / elapsed / 1e9
+    achieved = layer_bytes / (avg_us * 1e-6) / 1e9
+
+    # prefill quantizer: bytes = bf16 K+V in + packed out; flops = 2 D^2 per matvec (4 for Q_prod K + V)
+    q_s = statistics.median(q_ms) * 1e-3
+    n_vec = B * Hkv * N
+    q_bytes = n_vec * (4 * D + per_tok)
+    q_flops = n_vec * 2 * D * D * (4 if qjl else 2)
+
+    line = {
+        "metric": "fused decode-attn us/layer + packed-KV GB/s (% HBM peak), 8B KV shape @32K",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "us_per_layer": round(avg_us, 3),
+        "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"BASELINE config 2: decode attention over {args.layers} independently seeded packed "
+                         f"layers, B={B}, Hq={Hq}, Hkv={Hkv}, D={D}, N={N}, "
+                         + (f"{bits}-bit Q_prod K ({bits - 1}-bit MSE + 1-bit QJL) / {bits}-bit Q_mse V" if qjl
+                            else f"{bits}-bit Q_mse K and V")),
+            "packed_bytes_per_layer": layer_bytes,
+            "packed_bytes_per_token_head": per_tok,
+            "layers": args.layers,
+            "batch": B,
+            "context": N,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "tq_decode_attention (prepare + split + merge launches of one call), HIP events per call",
+        },
+        "prefill_quantizer": {
+            "ms_per_layer": round(q_s * 1e3, 3),
+            "GB_per_s": round(q_bytes / q_s / 1e9, 1),
+            "TFLOP_per_s": round(q_flops / q_s / 1e12, 2),
+            "fp32_valu_peak_tflops": VALU_FP32_PEAK_TFLOPS,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(bits)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,125 @@
+/*
+ * tq.h -- C ABI of libtq, the MI355X (gfx950) TurboQuant hot path.
+ *
+ * Plain C: device pointers, sizes and a hipStream_t passed as void*.  Every
+ * entry point is asynchronous on the given stream, never allocates, never
+ * throws, and returns a tq_status.  All pointers are device pointers unless
+ * stated otherwise.  All memory is owned by the caller.
+ *
+ * Data types: "bf16" and "f16" arrays are passed as uint16_t bit patterns;
+ * rotations / codebooks / QJL matrices are fp32, row-major.
+ *
+ * Packed-cache layout (reference runtime/packed_qmse_cache.py:13-43, 58-92,
+ * 121-154): for G = batch*kv_heads groups with a capacity of `cap` tokens,
+ *   codes   u8  [G][cap][ceil(D*bits/8)]  code d at bits [d*bits, d*bits+bits)
+ *                                         of the row's LSB-first bit stream
+ *   norms   f16 [G][cap]                  fp16 RNE of the fp32 L2 norm (0 -> 1)
+ *   signs   u8  [G][cap][D/8]             QJL bit i = (r_hat . S_i >= 0)
+ *   rnorms  f16 [G][cap]                  fp16 RNE of the residual norm (0 -> 1)
+ * With cap == N this is exactly the reference's contiguous [B,Hkv,N,row].
+ */
+#ifndef TQ_H_
+#define TQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQ_ABI_VERSION 1
+
+typedef enum tq_status {
+    TQ_OK = 0,
+    TQ_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, bad bit width        */
+    TQ_ERR_UNSUPPORTED = 2,      /* valid but not implemented (e.g. D != 128)    */
+    TQ_ERR_WORKSPACE = 3,        /* workspace missing or too small               */
+    TQ_ERR_HIP = 4               /* a HIP runtime call failed (launch, ...)      */
+} tq_status;
+
+/* Version of this ABI (TQ_ABI_VERSION). */
+int tq_abi_version(void);
+
+/* Static, NUL-terminated description of a status code. */
+const char* tq_status_string(int status);
+
+/*
+ * Q_mse encoder (prefill and decode-append).
+ * Replaces reference PackedMSELayer._encode_group (runtime/packed_qmse_cache.py:376-402)
+ * and the bit packing of _pack_indices (:13-43).
+ *
+ * x: bf16 [batch][heads][tokens][dim] with element strides (x_sb, x_sh, x_st),
+ *    the dim axis contiguous.  For each vector: n = |x|, u = x/n, z = u @ R^T,
+ *    code_j = #{i : boundaries[i] < z_j}.  Output vector (b,h,t) is written at
+ *    token slot (out_offset + t) of group (b*heads + h), groups `out_cap`
+ *    tokens apart.
+ */
+int tq_quantize_mse(const uint16_t* x, int batch, int heads, int64_t tokens, int dim,
+                    int64_t x_sb, int64_t x_sh, int64_t x_st,
+                    int bits, const float* rotation, const float* boundaries,
+                    uint8_t* codes, uint16_t* norms, int64_t out_cap, int64_t out_offset,
+                    void* stream);
+
+/*
+ * Q_prod key encoder: (mse_bits)-bit Q_mse codes plus the 1-bit QJL sketch of
+ * the residual.  Replaces reference PackedMSELayer._encode_keys_qjl_group
+ * (runtime/packed_qmse_cache.py:285-310), the residual decode it calls
+ * (_decode_group, :404-435) and _pack_qjl_signs (:148-154).
+ */
+int tq_quantize_prod(const uint16_t* x, int batch, int heads, int64_t tokens, int dim,
+                     int64_t x_sb, int64_t x_sh, int64_t x_st,
+                     int mse_bits, const float* rotation,
+                     const float* centers, const float* boundaries, const float* qjl,
+                     uint8_t* codes, uint16_t* norms, uint8_t* signs, uint16_t* rnorms,
+                     int64_t out_cap, int64_t out_offset, void* stream);
+
+/*
+ * Bytes of workspace tq_decode_attention needs for this shape.
+ */
+size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, int kv_heads, int dim, int64_t max_tokens);
+
+/*
+ * Fused decode attention over the packed cache, one query token per sequence.
+ * Replaces reference fused_attention (runtime/triton_kernels.py:238-368) and
+ * its _tile_attention_kernel (:84-198): q-side rotations, bit-unpack,
+ * codebook dequant, QJL logit correction, softmax, V accumulation, the
+ * cross-split log-sum-exp merge and the final un-rotation by R_v.
+ *
+ *   q        bf16 [batch][q_heads][dim] (contiguous)
+ *   seq_lens int32 [batch] valid tokens per sequence (nullable: all n_tokens)
+ *   n_tokens tokens stored per group (<= cap)
+ *   k_*, v_* packed cache (see layout above), groups `cap` tokens apart
+ *   k_signs / k_rnorms / qjl: nullable when has_qjl == 0
+ *   scale    logit scale; <= 0 selects 1/sqrt(dim) (the reference's choice)
+ *   out_f32  fp32 [batch][q_heads][dim] (nullable)
+ *   out_bf16 bf16 [batch][q_heads][dim] (nullable)
+ * logit_t = scale * (|k_t| <q R_k^T, C_k[kidx_t]> + sqrt(pi/2)/D |r_t| <q S^T, s_t>)
+ * out     = (sum_t softmax_t |v_t| C_v[vidx_t]) @ R_v
+ */
+int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
+                        const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
+                        const uint8_t* k_codes, const uint16_t* k_norms,
+                        const uint8_t* k_signs, const uint16_t* k_rnorms,
+                        const uint8_t* v_codes, const uint16_t* v_norms,
+                        int key_bits, int value_bits, int has_qjl,
+                        const float* key_rotation, const float* key_centers, const float* qjl,
+                        const float* value_rotation, const float* value_centers,
+                        float scale, float* out_f32, uint16_t* out_bf16,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Dequantise packed Q_mse rows to bf16 (verification / dense fallback of the
+ * caller).  Replaces reference _decode_group (runtime/packed_qmse_cache.py:404-435)
+ * and triton_decode_group (runtime/triton_kernels.py:227-236):
+ * out = bf16((C[codes] @ R) * f32(norm)).  rows are `cap` apart per group.
+ */
+int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, int64_t groups, int64_t tokens,
+                      int64_t cap, int dim, int bits, const float* rotation, const float* centers,
+                      uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ_H_ */

@@ -1,0 +1,164 @@
+"""GPU fused decode attention parity against the fp64 fused-formula oracle.
+
+Tolerance (north star): max |out_gpu - out_oracle| <= 2e-3 * ||out_oracle||_inf on
+the fp32 output, before the bf16 cast.  The kernel accumulates in fp32.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from turboquant.runtime import kernels as K
+from turboquant.runtime.params import layer_codecs
+from turboquant.runtime.synthetic import kv_bf16, query_bf16
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+TOL = 2e-3
+
+
+def u16(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def build_layer(cuda, B, Hkv, N, bits, qjl, seed, cap=None, kv_mu=None):
+    cap = cap or N
+    lc = layer_codecs(D, bits, 0, qjl, cuda)
+    kw = {} if kv_mu is None else {"mu": kv_mu}
+    k = kv_bf16((B, Hkv, N, D), seed=seed, device=cuda, **kw)
+    v = kv_bf16((B, Hkv, N, D), seed=seed + 1, device=cuda)
+    L = {
+        "kcodes": torch.zeros(B, Hkv, cap, K.row_bytes(D, lc.key_bits), dtype=torch.uint8, device=cuda),
+        "knorms": torch.zeros(B, Hkv, cap, dtype=torch.float16, device=cuda),
+        "vcodes": torch.zeros(B, Hkv, cap, K.row_bytes(D, lc.value_bits), dtype=torch.uint8, device=cuda),
+        "vnorms": torch.zeros(B, Hkv, cap, dtype=torch.float16, device=cuda),
+        "signs": None, "rnorms": None,
+    }
+    if qjl:
+        L["signs"] = torch.zeros(B, Hkv, cap, D // 8, dtype=torch.uint8, device=cuda)
+        L["rnorms"] = torch.zeros(B, Hkv, cap, dtype=torch.float16, device=cuda)
+        K.quantize_prod(k, lc.key, lc.qjl, L["kcodes"], L["knorms"], L["signs"], L["rnorms"])
+    else:
+        K.quantize_mse(k, lc.key, L["kcodes"], L["knorms"])
+    K.quantize_mse(v, lc.value, L["vcodes"], L["vnorms"])
+    return lc, L
+
+
+def host_layer(lc, L, N):
+    h = {
+        "kcodes": L["kcodes"][:, :, :N].cpu().numpy(), "knorms": u16(L["knorms"][:, :, :N]),
+        "vcodes": L["vcodes"][:, :, :N].cpu().numpy(), "vnorms": u16(L["vnorms"][:, :, :N]),
+        "signs": None if L["signs"] is None else L["signs"][:, :, :N].cpu().numpy(),
+        "rnorms": None if L["rnorms"] is None else u16(L["rnorms"][:, :, :N]),
+        "Rk": lc.key.rotation.cpu().numpy(), "Ck": lc.key.centers.cpu().numpy(),
+        "Rv": lc.value.rotation.cpu().numpy(), "Cv": lc.value.centers.cpu().numpy(),
+        "S": None if lc.qjl is None else lc.qjl.cpu().numpy(),
+        "kbits": lc.key_bits, "vbits": lc.value_bits,
+    }
+    return h
+
+
+def run(lc, L, q, N, seq_lens=None):
+    return K.decode_attention(q, k_codes=L["kcodes"], k_norms=L["knorms"], v_codes=L["vcodes"], v_norms=L["vnorms"],
+                              n_tokens=N, key=lc.key, value=lc.value, k_signs=L["signs"], k_rnorms=L["rnorms"],
+                              qjl=lc.qjl, seq_lens=seq_lens, want_f32=True)
+
+
+def check(out32, ref, tol=TOL):
+    ref_inf = np.abs(ref).max()
+    err = np.abs(out32.cpu().numpy().astype(np.float64) - ref).max()
+    assert err <= tol * ref_inf, f"max err {err:.3e} > {tol} * {ref_inf:.3e}"
+    return err / max(ref_inf, 1e-30)
+
+
+CASES = [
+    # (B, Hq, Hkv, N, bits, qjl)
+    (1, 32, 8, 4096, 4, True),    # BASELINE config 1 shape
+    (2, 8, 2, 1000, 4, True),     # ragged N (not a tile multiple)
+    (1, 8, 2, 700, 3, False),     # 3-bit Q_mse (codes straddle bytes and words)
+    (2, 10, 2, 513, 4, True),     # GQA 5
+    (1, 28, 4, 600, 4, True),     # GQA 7
+    (1, 4, 4, 300, 2, False),     # MHA, 2-bit
+    (1, 16, 2, 257, 3, True),     # GQA 8, 3-bit Q_prod
+    (1, 6, 2, 100, 1, False),     # GQA 3, 1-bit
+    (3, 12, 2, 333, 4, False),    # GQA 6, 4-bit Q_mse
+    (1, 2, 2, 1, 4, True),        # a single token
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,bits,qjl", CASES)
+def test_attention_matches_fp64_oracle(cuda, B, Hq, Hkv, N, bits, qjl):
+    lc, L = build_layer(cuda, B, Hkv, N, bits, qjl, seed=100 + N + bits)
+    q = query_bf16(B, Hq, D, seed=7 + N, device=cuda)
+    out16, out32 = run(lc, L, q, N)
+    torch.cuda.synchronize()
+    ref = O.fused_attention_f64(u16(q), host_layer(lc, L, N))
+    check(out32, ref)
+    # the bf16 output is the RNE rounding of the fp32 output
+    assert np.array_equal(u16(out16), O.f32_to_bf16_bits(out32.cpu().numpy()))
+
+
+def test_attention_capacity_and_seq_lens(cuda):
+    """cap > n_tokens, per-row valid lengths (including an empty row and a row longer
+    than the split size) and garbage in the unused slots."""
+    B, Hq, Hkv, N, cap = 4, 8, 2, 3000, 3500
+    lc, L = build_layer(cuda, B, Hkv, cap, 4, True, seed=555, cap=cap)
+    q = query_bf16(B, Hq, D, seed=3, device=cuda)
+    lens = torch.tensor([3000, 0, 1, 2049], dtype=torch.int32)
+    out16, out32 = run(lc, L, q, N, seq_lens=lens)
+    torch.cuda.synchronize()
+    hl = host_layer(lc, L, N)
+    ref = O.fused_attention_f64(u16(q), hl, n_valid=lens.numpy())
+    assert np.all(out32[1].cpu().numpy() == 0.0)  # empty sequence -> zeros
+    check(out32, ref)
+
+
+def test_attention_empty_cache_is_zero(cuda):
+    lc, L = build_layer(cuda, 1, 2, 4, 4, True, seed=1)
+    q = query_bf16(1, 8, D, seed=1, device=cuda)
+    out16, out32 = run(lc, L, q, 0)
+    torch.cuda.synchronize()
+    assert float(out32.abs().max()) == 0.0
+
+
+def test_attention_full_length_c2_rows(cuda):
+    """BASELINE config 2 sequence length (N=32768, GQA 4, 4-bit Q_prod) on 2 batch rows."""
+    B, Hq, Hkv, N = 2, 32, 8, 32768
+    lc, L = build_layer(cuda, B, Hkv, N, 4, True, seed=77)
+    q = query_bf16(B, Hq, D, seed=77, device=cuda)
+    _, out32 = run(lc, L, q, N)
+    torch.cuda.synchronize()
+    check(out32, O.fused_attention_f64(u16(q), host_layer(lc, L, N)))
+
+
+def test_attention_sharp_softmax(cuda):
+    """Large key norms make the softmax nearly one-hot (stresses max tracking across splits)."""
+    lc, L = build_layer(cuda, 1, 2, 5000, 4, True, seed=9, kv_mu=float(np.log(400.0)))
+    q = query_bf16(1, 8, D, seed=9, device=cuda)
+    _, out32 = run(lc, L, q, 5000)
+    torch.cuda.synchronize()
+    check(out32, O.fused_attention_f64(u16(q), host_layer(lc, L, 5000)))
+
+
+def test_attention_on_reference_golden_layer(cuda, golden_dir):
+    """Run the fused kernel on the packed layer the reference itself produced, and
+    compare to (a) the fp64 oracle (tolerance) and (b) the reference's CPU chunked
+    output, which rounds K^ and V^ to bf16 (looser, informational bound)."""
+    g = np.load(golden_dir / "attention_small.npz")
+    for name in ("prod4", "mse3"):
+        bits, qjl, hq, hkv, n = (int(v) for v in g[f"{name}_meta"])
+        lc = layer_codecs(D, bits, 0, bool(qjl), cuda)
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)  # noqa: E731
+        L = {"kcodes": dev(g[f"{name}_kcodes"]), "knorms": dev(g[f"{name}_knorms"].view(np.float16)),
+             "vcodes": dev(g[f"{name}_vcodes"]), "vnorms": dev(g[f"{name}_vnorms"].view(np.float16)),
+             "signs": dev(g[f"{name}_signs"]) if qjl else None,
+             "rnorms": dev(g[f"{name}_rnorms"].view(np.float16)) if qjl else None}
+        q = dev(g[f"{name}_q_bf16"].view(np.int16)).view(torch.bfloat16)
+        out16, out32 = run(lc, L, q, n)
+        torch.cuda.synchronize()
+        ref = O.fused_attention_f64(g[f"{name}_q_bf16"][:, :, 0, :], host_layer(lc, L, n))
+        check(out32, ref)
+        chunked = O.bf16_bits_to_f32(g[f"{name}_out_bf16"][:, :, 0, :]).astype(np.float64)
+        assert np.abs(out32.cpu().numpy() - chunked).max() <= 2e-2 * np.abs(chunked).max()

@@ -1,0 +1,55 @@
+// tq_common.h -- device helpers shared by the libtq HIP kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tq.h"
+
+#define TQ_DIM 128          // head_dim supported by the kernels
+#define TQ_MAX_GROUP 8      // max query heads per KV head (GQA group)
+
+namespace tq {
+
+// bf16 bit pattern -> fp32 (exact).
+__device__ __forceinline__ float bf16_to_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// fp32 -> bf16 bit pattern, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (x >> 16) | 0x40u;
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return x >> 16;
+}
+
+// fp32 -> IEEE binary16 bit pattern, round to nearest even (v_cvt_f16_f32).
+__device__ __forceinline__ uint32_t f32_to_f16(float f) {
+    _Float16 h = (_Float16)f;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+// IEEE-exact fp32 division and square root (the quantizer is bit-exact against
+// a CPU restatement that uses C's '/' and sqrtf).
+__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
+__device__ __forceinline__ float sqrt_rn(float a) { return __fsqrt_rn(a); }
+
+// Bits [pos, pos+n) of a little-endian word array held in registers, pos and
+// n compile-time constants after unrolling.
+template <int N>
+__device__ __forceinline__ uint32_t extract_bits(const uint32_t* w, int pos) {
+    const int wi = pos >> 5, sh = pos & 31;
+    uint32_t v = w[wi] >> sh;
+    if (sh + N > 32) v |= w[wi + 1] << (32 - sh);
+    return v & ((1u << N) - 1u);
+}
+
+}  // namespace tq
+
+#define TQ_CHECK_LAUNCH()                                 \
+    do {                                                  \
+        if (hipGetLastError() != hipSuccess) return TQ_ERR_HIP; \
+    } while (0)

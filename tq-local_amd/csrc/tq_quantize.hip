@@ -1,0 +1,300 @@
+// tq_quantize.hip -- TurboQuant encoder kernels for gfx950 (prefill and decode-append).
+//
+// One lane owns one token vector (D = 128): the bf16 vector is held in
+// VGPRs, and the rotation / QJL matrix rows are uniform across the wave, so
+// every multiply-add takes its matrix operand from an SGPR (scalar loads)
+// and its vector operand from a VGPR.  The fp32 evaluation order is fixed
+// (see the reference restatement in the CPU oracle):
+//
+//   norm^2 = fma chain d=0..127 of x_d*x_d;  n = sqrt_rn;  n==0 -> 1
+//   u_d    = x_d /_rn n
+//   z_j    = fma chain d=0..127 of u_d*R[j][d]          (z = u @ R^T)
+//   code_j = #{i : boundaries_i < z_j}                   (torch.bucketize right=False)
+//   Q_prod residual:  khat_d = bf16((fma chain j=0..127 of C[code_j]*R[j][d]) * f32(f16(n)))
+//                     r = x - khat;  rho = sqrt_rn(fma chain r_d^2) (0 -> 1);  rhat = r /_rn rho
+//                     sign_i = (fma chain d of rhat_d*S[i][d]) >= 0
+//
+// Reference: runtime/packed_qmse_cache.py:376-402 (_encode_group), :285-310
+// (_encode_keys_qjl_group), :404-435 (_decode_group), :13-43 (_pack_indices),
+// :148-154 (_pack_qjl_signs).
+
+#include "tq_common.h"
+
+namespace {
+
+constexpr int D = TQ_DIM;
+constexpr int QBLOCK = 256;  // lanes (= vectors) per workgroup
+
+struct QuantArgs {
+    const uint16_t* x;
+    int heads;
+    int64_t tokens;
+    int64_t n_vec;
+    int64_t x_sb, x_sh, x_st;
+    const float* R;
+    const float* centers;
+    const float* boundaries;
+    const float* S;
+    uint8_t* codes;
+    uint16_t* norms;
+    uint8_t* signs;
+    uint16_t* rnorms;
+    int64_t out_cap, out_offset;
+};
+
+// Appends `nbits` bits to a 64-bit staging register; full 32-bit words are
+// written to `dst` (the lane's own output row).
+struct BitWriter {
+    uint64_t acc = 0;
+    int fill = 0;
+    int wi = 0;
+    __device__ __forceinline__ void put(uint32_t v, int nbits, uint32_t* dst) {
+        acc |= (uint64_t)v << fill;
+        fill += nbits;
+        if (fill >= 32) {
+            dst[wi++] = (uint32_t)acc;
+            acc >>= 32;
+            fill -= 32;
+        }
+    }
+};
+
+template <int BITS, bool PROD>
+__global__ __launch_bounds__(QBLOCK) void quantize_kernel(
+    const uint16_t* __restrict__ x, int heads, int64_t tokens, int64_t n_vec, int64_t x_sb, int64_t x_sh,
+    int64_t x_st, const float* __restrict__ R, const float* __restrict__ centers,
+    const float* __restrict__ boundaries, const float* __restrict__ S, uint8_t* __restrict__ codes,
+    uint16_t* __restrict__ norms, uint8_t* __restrict__ signs, uint16_t* __restrict__ rnorms, int64_t out_cap,
+    int64_t out_offset) {
+    __shared__ uint8_t s_code[D][QBLOCK];  // PROD only: codes of each lane, column per lane
+    __shared__ float s_centers[1 << BITS];
+    if (PROD && threadIdx.x < (1 << BITS)) s_centers[threadIdx.x] = centers[threadIdx.x];
+    if (PROD) __syncthreads();
+
+    const int64_t v = (int64_t)blockIdx.x * QBLOCK + threadIdx.x;
+    if (v >= n_vec) return;  // no barrier below this point
+    const int64_t t = v % tokens;
+    const int64_t gh = v / tokens;
+    const int64_t h = gh % heads;
+    const int64_t b = gh / heads;
+    const uint16_t* xv = x + b * x_sb + h * x_sh + t * x_st;
+    const int64_t slot = gh * out_cap + out_offset + t;
+
+    // ---- load x, norm
+    float u[D];
+    {
+        const uint4* x4 = reinterpret_cast<const uint4*>(xv);
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+            uint4 w = x4[i];
+            u[8 * i + 0] = tq::bf16_to_f32(w.x & 0xFFFFu);
+            u[8 * i + 1] = tq::bf16_to_f32(w.x >> 16);
+            u[8 * i + 2] = tq::bf16_to_f32(w.y & 0xFFFFu);
+            u[8 * i + 3] = tq::bf16_to_f32(w.y >> 16);
+            u[8 * i + 4] = tq::bf16_to_f32(w.z & 0xFFFFu);
+            u[8 * i + 5] = tq::bf16_to_f32(w.z >> 16);
+            u[8 * i + 6] = tq::bf16_to_f32(w.w & 0xFFFFu);
+            u[8 * i + 7] = tq::bf16_to_f32(w.w >> 16);
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) ss = __builtin_fmaf(u[d], u[d], ss);
+    float n = tq::sqrt_rn(ss);
+    if (!(n > 0.0f)) n = 1.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) u[d] = tq::div_rn(u[d], n);
+    const uint32_t n16 = tq::f32_to_f16(n);
+    norms[slot] = (uint16_t)n16;
+
+    // ---- rotate, bucketize, pack
+    constexpr int NB = (1 << BITS) - 1;
+    constexpr int ROW = D * BITS / 8;
+    uint32_t* crow = reinterpret_cast<uint32_t*>(codes + slot * ROW);
+    BitWriter bw;
+    for (int j = 0; j < D; ++j) {
+        const float* rj = R + j * D;
+        float z = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) z = __builtin_fmaf(u[d], rj[d], z);
+        uint32_t c = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) c += (boundaries[i] < z) ? 1u : 0u;
+        bw.put(c, BITS, crow);
+        if (PROD) s_code[j][threadIdx.x] = (uint8_t)c;
+    }
+
+    if constexpr (PROD) {
+        // ---- residual decode khat = bf16((C[code] @ R) * f32(f16(n))), accumulated row by row
+        float acc[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        for (int j = 0; j < D; ++j) {
+            const float cj = s_centers[s_code[j][threadIdx.x]];
+            const float* rj = R + j * D;
+#pragma unroll
+            for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
+        }
+        const float nf = tq::f16_to_f32(n16);
+        const uint4* x4 = reinterpret_cast<const uint4*>(xv);
+        float rs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+            uint4 w = x4[i];
+            uint32_t xs[8] = {w.x & 0xFFFFu, w.x >> 16, w.y & 0xFFFFu, w.y >> 16,
+                              w.z & 0xFFFFu, w.z >> 16, w.w & 0xFFFFu, w.w >> 16};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int d = 8 * i + k;
+                const float kh = tq::bf16_to_f32(tq::f32_to_bf16(acc[d] * nf));
+                acc[d] = tq::bf16_to_f32(xs[k]) - kh;
+                rs = __builtin_fmaf(acc[d], acc[d], rs);
+            }
+        }
+        float rho = tq::sqrt_rn(rs);
+        if (!(rho > 0.0f)) rho = 1.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = tq::div_rn(acc[d], rho);
+        rnorms[slot] = (uint16_t)tq::f32_to_f16(rho);
+        uint32_t* srow = reinterpret_cast<uint32_t*>(signs + slot * (D / 8));
+        BitWriter sw;
+        for (int i = 0; i < D; ++i) {
+            const float* si = S + i * D;
+            float p = 0.0f;
+#pragma unroll
+            for (int d = 0; d < D; ++d) p = __builtin_fmaf(acc[d], si[d], p);
+            sw.put(p >= 0.0f ? 1u : 0u, 1, srow);
+        }
+    }
+}
+
+// ------------------------------------------------------------ residual-free decode
+template <int BITS>
+__global__ __launch_bounds__(QBLOCK) void dequantize_kernel(const uint8_t* __restrict__ codes,
+                                                            const uint16_t* __restrict__ norms,
+                                                            int64_t tokens, int64_t cap, int64_t n_vec,
+                                                            const float* __restrict__ R,
+                                                            const float* __restrict__ centers,
+                                                            uint16_t* __restrict__ out) {
+    __shared__ float s_centers[1 << BITS];
+    if (threadIdx.x < (1 << BITS)) s_centers[threadIdx.x] = centers[threadIdx.x];
+    __syncthreads();
+    const int64_t v = (int64_t)blockIdx.x * QBLOCK + threadIdx.x;
+    if (v >= n_vec) return;
+    const int64_t g = v / tokens, t = v % tokens;
+    const int64_t slot = g * cap + t;
+    constexpr int ROW = D * BITS / 8;
+    const uint8_t* row = codes + slot * ROW;
+    float acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+    for (int j = 0; j < D; ++j) {
+        const int pos = j * BITS;
+        uint32_t pair = row[pos >> 3];
+        if ((pos & 7) + BITS > 8) pair |= (uint32_t)row[(pos >> 3) + 1] << 8;
+        const float cj = s_centers[(pair >> (pos & 7)) & ((1u << BITS) - 1u)];
+        const float* rj = R + j * D;
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
+    }
+    const float nf = tq::f16_to_f32(norms[slot]);
+    uint4* o4 = reinterpret_cast<uint4*>(out + v * D);
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+        uint32_t p[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            p[k] = tq::f32_to_bf16(acc[8 * i + 2 * k] * nf) | (tq::f32_to_bf16(acc[8 * i + 2 * k + 1] * nf) << 16);
+        o4[i] = make_uint4(p[0], p[1], p[2], p[3]);
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(const uint16_t* x, int batch, int heads, int64_t tokens, int dim, int64_t x_sb, int64_t x_sh,
+                 int64_t x_st, int64_t out_cap, int64_t out_offset) {
+    if (!x || batch < 0 || heads < 0 || tokens < 0 || out_offset < 0) return TQ_ERR_INVALID_ARGUMENT;
+    if (out_offset + tokens > out_cap) return TQ_ERR_INVALID_ARGUMENT;
+    if (dim != TQ_DIM) return TQ_ERR_UNSUPPORTED;
+    if (!aligned16(x) || (x_sb % 8) || (x_sh % 8) || (x_st % 8)) return TQ_ERR_UNSUPPORTED;
+    return TQ_OK;
+}
+
+template <int BITS, bool PROD>
+int launch_quantize(const QuantArgs& a, hipStream_t s) {
+    const int64_t blocks = (a.n_vec + QBLOCK - 1) / QBLOCK;
+    if (blocks == 0) return TQ_OK;
+    hipLaunchKernelGGL((quantize_kernel<BITS, PROD>), dim3((unsigned)blocks), dim3(QBLOCK), 0, s, a.x, a.heads,
+                       a.tokens, a.n_vec, a.x_sb, a.x_sh, a.x_st, a.R, a.centers, a.boundaries, a.S, a.codes,
+                       a.norms, a.signs, a.rnorms, a.out_cap, a.out_offset);
+    TQ_CHECK_LAUNCH();
+    return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" int tq_quantize_mse(const uint16_t* x, int batch, int heads, int64_t tokens, int dim, int64_t x_sb,
+                               int64_t x_sh, int64_t x_st, int bits, const float* rotation,
+                               const float* boundaries, uint8_t* codes, uint16_t* norms, int64_t out_cap,
+                               int64_t out_offset, void* stream) {
+    int st = check_common(x, batch, heads, tokens, dim, x_sb, x_sh, x_st, out_cap, out_offset);
+    if (st != TQ_OK) return st;
+    if (!rotation || !boundaries || !codes || !norms) return TQ_ERR_INVALID_ARGUMENT;
+    if (!aligned16(codes)) return TQ_ERR_UNSUPPORTED;
+    QuantArgs a{x, heads, tokens, (int64_t)batch * heads * tokens, x_sb, x_sh, x_st, rotation, nullptr,
+                boundaries, nullptr, codes, norms, nullptr, nullptr, out_cap, out_offset};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (bits) {
+        case 1: return launch_quantize<1, false>(a, s);
+        case 2: return launch_quantize<2, false>(a, s);
+        case 3: return launch_quantize<3, false>(a, s);
+        case 4: return launch_quantize<4, false>(a, s);
+        default: return TQ_ERR_INVALID_ARGUMENT;
+    }
+}
+
+extern "C" int tq_quantize_prod(const uint16_t* x, int batch, int heads, int64_t tokens, int dim, int64_t x_sb,
+                                int64_t x_sh, int64_t x_st, int mse_bits, const float* rotation,
+                                const float* centers, const float* boundaries, const float* qjl, uint8_t* codes,
+                                uint16_t* norms, uint8_t* signs, uint16_t* rnorms, int64_t out_cap,
+                                int64_t out_offset, void* stream) {
+    int st = check_common(x, batch, heads, tokens, dim, x_sb, x_sh, x_st, out_cap, out_offset);
+    if (st != TQ_OK) return st;
+    if (!rotation || !centers || !boundaries || !qjl || !codes || !norms || !signs || !rnorms)
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (!aligned16(codes) || !aligned16(signs)) return TQ_ERR_UNSUPPORTED;
+    QuantArgs a{x, heads, tokens, (int64_t)batch * heads * tokens, x_sb, x_sh, x_st, rotation, centers,
+                boundaries, qjl, codes, norms, signs, rnorms, out_cap, out_offset};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (mse_bits) {
+        case 1: return launch_quantize<1, true>(a, s);
+        case 2: return launch_quantize<2, true>(a, s);
+        case 3: return launch_quantize<3, true>(a, s);
+        default: return TQ_ERR_INVALID_ARGUMENT;
+    }
+}
+
+extern "C" int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, int64_t groups, int64_t tokens,
+                                 int64_t cap, int dim, int bits, const float* rotation, const float* centers,
+                                 uint16_t* out, void* stream) {
+    if (!codes || !norms || !rotation || !centers || !out || groups < 0 || tokens < 0 || tokens > cap)
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (dim != TQ_DIM) return TQ_ERR_UNSUPPORTED;
+    if (!aligned16(codes) || !aligned16(out)) return TQ_ERR_UNSUPPORTED;
+    const int64_t n_vec = groups * tokens;
+    const int64_t blocks = (n_vec + QBLOCK - 1) / QBLOCK;
+    if (blocks == 0) return TQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (bits) {
+#define TQ_DQ(B)                                                                                          \
+    case B:                                                                                               \
+        hipLaunchKernelGGL(dequantize_kernel<B>, dim3((unsigned)blocks), dim3(QBLOCK), 0, s, codes, norms, \
+                           tokens, cap, n_vec, rotation, centers, out);                                   \
+        break;
+        TQ_DQ(1) TQ_DQ(2) TQ_DQ(3) TQ_DQ(4)
+#undef TQ_DQ
+        default: return TQ_ERR_INVALID_ARGUMENT;
+    }
+    TQ_CHECK_LAUNCH();
+    return TQ_OK;
+}

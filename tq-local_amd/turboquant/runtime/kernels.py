@@ -1,0 +1,159 @@
+"""Torch-facing wrappers of the libtq C ABI (PyTorch-ROCm supplies memory and streams).
+
+Every function validates dtype / shape / device on the host, then makes one
+C-ABI call on ``torch.cuda.current_stream()``.  There is no CPU path: a CPU
+tensor, or a missing libtq.so, raises.
+
+Reference interfaces replaced:
+  quantize_mse   -> PackedMSELayer._encode_group           runtime/packed_qmse_cache.py:376-402
+  quantize_prod  -> PackedMSELayer._encode_keys_qjl_group  runtime/packed_qmse_cache.py:285-310
+  dequantize_mse -> PackedMSELayer._decode_group           runtime/packed_qmse_cache.py:404-435
+  decode_attention -> fused_attention                      runtime/triton_kernels.py:238-368
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from turboquant.runtime import _lib
+
+HEAD_DIM = 128
+
+
+def _vp(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(*tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                f"TurboQuant kernels run on the GPU only (libtq, gfx950); got a tensor on {t.device}"
+            )
+
+
+def row_bytes(dim: int, bits: int) -> int:
+    return (dim * bits + 7) // 8
+
+
+@dataclass
+class CodecParams:
+    """Device-resident parameters of one Q_mse codec (rotation, codebook)."""
+
+    bits: int
+    rotation: torch.Tensor  # fp32 [D, D]
+    centers: torch.Tensor  # fp32 [2^bits]
+    boundaries: torch.Tensor  # fp32 [2^bits - 1]
+
+
+def _as_encoder_input(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() != 4:
+        raise ValueError(f"expected [batch, heads, tokens, dim], got {tuple(x.shape)}")
+    if x.shape[-1] != HEAD_DIM:
+        raise ValueError(f"head_dim {x.shape[-1]} unsupported (kernels are built for {HEAD_DIM})")
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    aligned = x.stride(-1) == 1 and all(s % 8 == 0 for s in x.stride()[:3]) and x.data_ptr() % 16 == 0
+    return x if aligned else x.contiguous()
+
+
+def quantize_mse(x: torch.Tensor, codec: CodecParams, codes: torch.Tensor, norms: torch.Tensor,
+                 offset: int = 0) -> None:
+    """Encode x [B,H,T,D] into codes [B,H,cap,row] / norms [B,H,cap] at token slot ``offset``."""
+    x = _as_encoder_input(x)
+    _require_gpu(x, codes, norms, codec.rotation)
+    B, H, T, D = x.shape
+    cap = codes.shape[2]
+    if codes.shape != (B, H, cap, row_bytes(D, codec.bits)) or codes.dtype != torch.uint8 or not codes.is_contiguous():
+        raise ValueError(f"codes buffer {tuple(codes.shape)} {codes.dtype} does not match {B, H, cap}")
+    if norms.shape != (B, H, cap) or norms.dtype != torch.float16 or not norms.is_contiguous():
+        raise ValueError("norms buffer must be contiguous float16 [B, H, cap]")
+    _lib.call("tq_quantize_mse", _vp(x), B, H, T, D, x.stride(0), x.stride(1), x.stride(2), codec.bits,
+              _vp(codec.rotation), _vp(codec.boundaries), _vp(codes), _vp(norms), cap, offset, _stream(x.device))
+
+
+def quantize_prod(x: torch.Tensor, codec: CodecParams, qjl: torch.Tensor, codes: torch.Tensor,
+                  norms: torch.Tensor, signs: torch.Tensor, rnorms: torch.Tensor, offset: int = 0) -> None:
+    """Q_prod keys: (codec.bits)-bit MSE codes + 1-bit QJL signs of the residual, at slot ``offset``."""
+    x = _as_encoder_input(x)
+    _require_gpu(x, codes, norms, signs, rnorms, qjl)
+    B, H, T, D = x.shape
+    cap = codes.shape[2]
+    if codes.shape != (B, H, cap, row_bytes(D, codec.bits)) or not codes.is_contiguous():
+        raise ValueError("codes buffer shape mismatch")
+    if signs.shape != (B, H, cap, D // 8) or not signs.is_contiguous():
+        raise ValueError("signs buffer shape mismatch")
+    for t in (norms, rnorms):
+        if t.shape != (B, H, cap) or t.dtype != torch.float16 or not t.is_contiguous():
+            raise ValueError("norm buffers must be contiguous float16 [B, H, cap]")
+    _lib.call("tq_quantize_prod", _vp(x), B, H, T, D, x.stride(0), x.stride(1), x.stride(2), codec.bits,
+              _vp(codec.rotation), _vp(codec.centers), _vp(codec.boundaries), _vp(qjl), _vp(codes), _vp(norms),
+              _vp(signs), _vp(rnorms), cap, offset, _stream(x.device))
+
+
+def dequantize_mse(codes: torch.Tensor, norms: torch.Tensor, tokens: int, codec: CodecParams,
+                   dim: int = HEAD_DIM) -> torch.Tensor:
+    """codes [B,H,cap,row] -> bf16 [B,H,tokens,D] = bf16((C[codes] @ R) * norm)."""
+    _require_gpu(codes, norms)
+    B, H, cap, _ = codes.shape
+    out = torch.empty(B, H, tokens, dim, dtype=torch.bfloat16, device=codes.device)
+    _lib.call("tq_dequantize_mse", _vp(codes), _vp(norms), B * H, tokens, cap, dim, codec.bits,
+              _vp(codec.rotation), _vp(codec.centers), _vp(out), _stream(codes.device))
+    return out
+
+
+_workspaces: dict[tuple, torch.Tensor] = {}
+
+
+def attention_workspace(device: torch.device, batch: int, q_heads: int, kv_heads: int, max_tokens: int) -> torch.Tensor:
+    need = int(_lib.load().tq_decode_attention_workspace_bytes(batch, q_heads, kv_heads, HEAD_DIM, max_tokens))
+    if need == 0:
+        raise ValueError("invalid attention shape for workspace sizing")
+    key = (device.type, device.index)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.Tensor, v_codes: torch.Tensor,
+                     v_norms: torch.Tensor, n_tokens: int, key: CodecParams, value: CodecParams,
+                     k_signs: torch.Tensor | None = None, k_rnorms: torch.Tensor | None = None,
+                     qjl: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None,
+                     scale: float | None = None, want_f32: bool = False):
+    """Fused decode attention for one query token per sequence.
+
+    q: [B, Hq, D] or [B, Hq, 1, D] (any float dtype; bf16 is passed through).
+    Packed buffers are [B, Hkv, cap, ...] with ``n_tokens`` valid slots.
+    Returns bf16 [B, Hq, D] (and fp32 [B, Hq, D] if ``want_f32``).
+    """
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise ValueError("decode_attention takes exactly one query token per sequence")
+        q = q[:, :, 0, :]
+    q = q.to(torch.bfloat16).contiguous()
+    _require_gpu(q, k_codes, v_codes)
+    B, Hq, D = q.shape
+    Hkv, cap = k_codes.shape[1], k_codes.shape[2]
+    has_qjl = k_signs is not None
+    out_bf16 = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=q.device)
+    out_f32 = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device) if want_f32 else None
+    ws = attention_workspace(q.device, B, Hq, Hkv, max(int(n_tokens), 1))
+    if seq_lens is not None:
+        seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
+    s = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    _lib.call("tq_decode_attention", _vp(q), B, Hq, Hkv, D, _vp(seq_lens), int(n_tokens), cap,
+              _vp(k_codes), _vp(k_norms), _vp(k_signs), _vp(k_rnorms), _vp(v_codes), _vp(v_norms),
+              key.bits, value.bits, int(has_qjl), _vp(key.rotation), _vp(key.centers), _vp(qjl),
+              _vp(value.rotation), _vp(value.centers), ctypes.c_float(s), _vp(out_f32), _vp(out_bf16),
+              _vp(ws), ws.numel(), _stream(q.device))
+    return (out_bf16, out_f32) if want_f32 else out_bf16
