@@ -87,25 +87,32 @@ size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, int kv_heads,
  * cross-split log-sum-exp merge and the final un-rotation by R_v.
  *
  *   q        bf16 [batch][q_heads][dim] (contiguous)
- *   seq_lens int32 [batch] valid tokens per sequence (nullable: all n_tokens)
+ *   seq_starts int32 [batch] first valid token per sequence (nullable: 0), for
+ *            left-padded batches
+ *   seq_lens int32 [batch] end of the valid tokens per sequence (nullable: n_tokens)
  *   n_tokens tokens stored per group (<= cap)
  *   k_*, v_* packed cache (see layout above), groups `cap` tokens apart
  *   k_signs / k_rnorms / qjl: nullable when has_qjl == 0
  *   scale    logit scale; <= 0 selects 1/sqrt(dim) (the reference's choice)
  *   out_f32  fp32 [batch][q_heads][dim] (nullable)
  *   out_bf16 bf16 [batch][q_heads][dim] (nullable)
+ *   lse_out  fp32 [batch][q_heads] log-sum-exp of the scaled logits (nullable;
+ *            -inf for an empty sequence), for merging with other attention parts
+ *   workspace device scratch of tq_decode_attention_workspace_bytes(); it is
+ *            used only during the call (calls sharing one workspace must be
+ *            ordered on one stream)
  * logit_t = scale * (|k_t| <q R_k^T, C_k[kidx_t]> + sqrt(pi/2)/D |r_t| <q S^T, s_t>)
  * out     = (sum_t softmax_t |v_t| C_v[vidx_t]) @ R_v
  */
 int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
-                        const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
+                        const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
                         const uint8_t* k_codes, const uint16_t* k_norms,
                         const uint8_t* k_signs, const uint16_t* k_rnorms,
                         const uint8_t* v_codes, const uint16_t* v_norms,
                         int key_bits, int value_bits, int has_qjl,
                         const float* key_rotation, const float* key_centers, const float* qjl,
                         const float* value_rotation, const float* value_centers,
-                        float scale, float* out_f32, uint16_t* out_bf16,
+                        float scale, float* out_f32, uint16_t* out_bf16, float* lse_out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -117,6 +124,16 @@ int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads,
 int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, int64_t groups, int64_t tokens,
                       int64_t cap, int dim, int bits, const float* rotation, const float* centers,
                       uint16_t* out, void* stream);
+
+/*
+ * Dequantise packed Q_prod keys to bf16: the Q_mse reconstruction plus the QJL
+ * correction, rounded as the reference does (runtime/packed_qmse_cache.py:312-330):
+ *   corr = bf16(((signs(+-1) @ S) * rnorm) * sqrt(pi/2)/D);  out = bf16(khat + corr)
+ */
+int tq_dequantize_prod(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
+                       const uint16_t* rnorms, int64_t groups, int64_t tokens, int64_t cap, int dim,
+                       int mse_bits, const float* rotation, const float* centers, const float* qjl,
+                       uint16_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -55,9 +55,10 @@ def lib() -> ctypes.CDLL:
         L.tq_oracle_encode_prod.argtypes = [P, I64, I, I, P, P, P, P, P, P, P, P]
         L.tq_oracle_decode_mse.argtypes = [P, P, I64, I, I, P, P, P]
         L.tq_oracle_rotated.argtypes = [P, I64, I, P, P]
+        L.tq_oracle_decode_prod.argtypes = [P, P, P, P, I64, I, I, P, P, P, P]
         L.tq_oracle_f32_to_f16_array.argtypes = [P, I64, P]
         L.tq_oracle_f32_to_bf16_array.argtypes = [P, I64, P]
-        for fn in ("tq_oracle_encode_mse", "tq_oracle_encode_prod", "tq_oracle_decode_mse",
+        for fn in ("tq_oracle_encode_mse", "tq_oracle_encode_prod", "tq_oracle_decode_mse", "tq_oracle_decode_prod",
                    "tq_oracle_rotated", "tq_oracle_f32_to_f16_array", "tq_oracle_f32_to_bf16_array"):
             getattr(L, fn).restype = None
         _lib = L
@@ -158,6 +159,19 @@ def decode_mse(codes: np.ndarray, norms: np.ndarray, bits: int, dim: int, R: np.
     return out
 
 
+def decode_prod(codes, norms, signs, rnorms, mse_bits: int, dim: int, R, centers, S):
+    """Q_prod keys -> bf16 bits [M, D]: MSE reconstruction + bf16 QJL correction."""
+    codes = np.ascontiguousarray(codes, np.uint8)
+    m = codes.shape[0]
+    out = np.zeros((m, dim), np.uint16)
+    lib().tq_oracle_decode_prod(_p(codes), _p(np.ascontiguousarray(norms, np.uint16)),
+                                _p(np.ascontiguousarray(signs, np.uint8)), _p(np.ascontiguousarray(rnorms, np.uint16)),
+                                m, dim, mse_bits, _p(np.ascontiguousarray(R, np.float32)),
+                                _p(np.ascontiguousarray(centers, np.float32)), _p(np.ascontiguousarray(S, np.float32)),
+                                _p(out))
+    return out
+
+
 def rotated(x_bf16: np.ndarray, R: np.ndarray) -> np.ndarray:
     """fp32 pre-images z = (x/|x|) @ R^T in the encoder's exact order."""
     x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
@@ -172,14 +186,15 @@ def _sign_pm1(signs_u8: np.ndarray, dim: int) -> np.ndarray:
     return 2.0 * unpack_codes(signs_u8, 1, dim).astype(np.float64) - 1.0
 
 
-def fused_attention_f64(q_bf16, layer: dict, n_valid: np.ndarray | None = None) -> np.ndarray:
+def fused_attention_f64(q_bf16, layer: dict, n_valid: np.ndarray | None = None,
+                        n_start: np.ndarray | None = None) -> np.ndarray:
     """Fused decode attention in fp64.
 
     q_bf16: [B, Hq, D] uint16.  ``layer`` holds (numpy) packed tensors
     ``kcodes [B,Hkv,N,rowk]``, ``knorms [B,Hkv,N]`` (f16 bits), ``vcodes``,
     ``vnorms``, optional ``signs``/``rnorms`` and the fp32 params
-    ``Rk, Ck, Rv, Cv, S`` plus ``kbits, vbits``.  ``n_valid[b]`` limits the
-    tokens of batch row b (default: all).  Returns fp64 [B, Hq, D].
+    ``Rk, Ck, Rv, Cv, S`` plus ``kbits, vbits``.  Batch row b attends to tokens
+    [n_start[b], n_valid[b]) (defaults: 0 and N).  Returns fp64 [B, Hq, D].
 
     logit_t = (n_k <q Rk^T, Ck[kidx_t]> + sqrt(pi/2)/D * rho_t <q S^T, s_t>) / sqrt(D)
     out     = (sum_t softmax(logit)_t n_v,t Cv[vidx_t]) @ Rv
@@ -199,20 +214,22 @@ def fused_attention_f64(q_bf16, layer: dict, n_valid: np.ndarray | None = None) 
     out = np.zeros((B, Hq, D))
     for b in range(B):
         nb = N if n_valid is None else int(n_valid[b])
-        if nb == 0:
+        sb = 0 if n_start is None else int(n_start[b])
+        if nb <= sb:
             continue  # an empty sequence attends to nothing: output stays zero
+        sl = slice(sb, nb)
         for h in range(Hkv):
-            kidx = unpack_codes(kc[b, h, :nb], layer["kbits"], D)
-            vidx = unpack_codes(layer["vcodes"][b, h, :nb], layer["vbits"], D)
-            kn = f16_bits_to_f32(layer["knorms"][b, h, :nb]).astype(np.float64)
-            vn = f16_bits_to_f32(layer["vnorms"][b, h, :nb]).astype(np.float64)
+            kidx = unpack_codes(kc[b, h, sl], layer["kbits"], D)
+            vidx = unpack_codes(layer["vcodes"][b, h, sl], layer["vbits"], D)
+            kn = f16_bits_to_f32(layer["knorms"][b, h, sl]).astype(np.float64)
+            vn = f16_bits_to_f32(layer["vnorms"][b, h, sl]).astype(np.float64)
             qq = q[b, h * g:(h + 1) * g]  # [g, D]
             q_rot = qq @ Rk.T
             logits = (q_rot @ Ck[kidx].T) * kn[None, :]
             if has_qjl:
                 q_proj = qq @ layer["S"].astype(np.float64).T
-                sg = _sign_pm1(layer["signs"][b, h, :nb], D)
-                rn = f16_bits_to_f32(layer["rnorms"][b, h, :nb]).astype(np.float64)
+                sg = _sign_pm1(layer["signs"][b, h, sl], D)
+                rn = f16_bits_to_f32(layer["rnorms"][b, h, sl]).astype(np.float64)
                 logits = logits + qs * rn[None, :] * (q_proj @ sg.T)
             logits = logits * hs
             m = logits.max(axis=1, keepdims=True)
@@ -221,6 +238,29 @@ def fused_attention_f64(q_bf16, layer: dict, n_valid: np.ndarray | None = None) 
             o_rot = (p * vn[None, :]) @ Cv[vidx]
             out[b, h * g:(h + 1) * g] = (o_rot / np.maximum(ssum, 1e-8)) @ Rv
     return out
+
+
+def dequant_layer_f64(layer: dict) -> tuple[np.ndarray, np.ndarray]:
+    """fp64 K^ [B,Hkv,N,D] (MSE reconstruction + QJL correction) and V^, unrounded."""
+    kc = layer["kcodes"]
+    B, Hkv, N = kc.shape[:3]
+    D = layer["Rk"].shape[0]
+    qs = math.sqrt(math.pi / 2) / D
+    kh = np.zeros((B, Hkv, N, D))
+    vh = np.zeros((B, Hkv, N, D))
+    for b in range(B):
+        for h in range(Hkv):
+            kidx = unpack_codes(kc[b, h], layer["kbits"], D)
+            kn = f16_bits_to_f32(layer["knorms"][b, h]).astype(np.float64)
+            kh[b, h] = (layer["Ck"].astype(np.float64)[kidx] @ layer["Rk"].astype(np.float64)) * kn[:, None]
+            if layer.get("signs") is not None:
+                sg = _sign_pm1(layer["signs"][b, h], D)
+                rn = f16_bits_to_f32(layer["rnorms"][b, h]).astype(np.float64)
+                kh[b, h] += (sg @ layer["S"].astype(np.float64)) * (rn[:, None] * qs)
+            vidx = unpack_codes(layer["vcodes"][b, h], layer["vbits"], D)
+            vn = f16_bits_to_f32(layer["vnorms"][b, h]).astype(np.float64)
+            vh[b, h] = (layer["Cv"].astype(np.float64)[vidx] @ layer["Rv"].astype(np.float64)) * vn[:, None]
+    return kh, vh
 
 
 def dequant_attention_f64(q_bf16, layer: dict) -> np.ndarray:

@@ -175,6 +175,32 @@ void tq_oracle_decode_mse(const uint8_t* codes, const uint16_t* norms, int64_t n
     }
 }
 
+/* Q_prod key decode (reference _decode_keys_qjl_group, runtime/packed_qmse_cache.py:312-330):
+ * corr_d = bf16(((fma chain over i of s_i * S[i][d]) * rho) * (float)(sqrt(pi/2)/D)),
+ * out_d  = bf16(khat_d + corr_d).                                                          */
+void tq_oracle_decode_prod(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
+                           const uint16_t* rnorms, int64_t n_vec, int D, int mse_bits, const float* R,
+                           const float* centers, const float* S, uint16_t* out_bf16) {
+    int row_bytes = (D * mse_bits + 7) / 8;
+    int sign_bytes = (D + 7) / 8;
+    const float qs = (float)(1.2533141373155002512078826 / (double)D);
+    float kh[TQ_ORACLE_MAX_D], corr[TQ_ORACLE_MAX_D];
+    for (int64_t v = 0; v < n_vec; ++v) {
+        decode_mse_one(codes + v * row_bytes, norms[v], D, mse_bits, R, centers, kh);
+        for (int d = 0; d < D; ++d) corr[d] = 0.0f;
+        const uint8_t* srow = signs + v * sign_bytes;
+        for (int i = 0; i < D; ++i) {
+            float si = ((srow[i >> 3] >> (i & 7)) & 1u) ? 1.0f : -1.0f;
+            for (int d = 0; d < D; ++d) corr[d] = fmaf(si, S[(size_t)i * D + d], corr[d]);
+        }
+        float rho = tq_oracle_f16_to_f32(rnorms[v]);
+        for (int d = 0; d < D; ++d) {
+            float c = bf16_to_f32(tq_oracle_f32_to_bf16((corr[d] * rho) * qs));
+            out_bf16[v * D + d] = tq_oracle_f32_to_bf16(kh[d] + c);
+        }
+    }
+}
+
 /* Q_prod key encoder: (bits)-bit Q_mse codes + 1-bit QJL sketch of the residual. */
 void tq_oracle_encode_prod(const uint16_t* x, int64_t n_vec, int D, int mse_bits, const float* R,
                            const float* centers, const float* boundaries, const float* S, uint8_t* codes,

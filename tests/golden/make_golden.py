@@ -121,6 +121,8 @@ def main(ref_src: str) -> None:
     enc["prod4_rnorms"] = _f16_bits(qjl.residual_norms)
     dec = pqc.PackedMSELayer._decode_group(mse, rot, c)
     enc["prod4_khat_bf16"] = _bf16_bits(dec)
+    full = pqc.PackedMSELayer._decode_keys_qjl_group(_Enc(), mse, qjl, rot, c, smat)
+    enc["prod4_kfull_bf16"] = _bf16_bits(full)
     np.savez_compressed(HERE / "encode_small.npz", **enc)
 
     # ------------------------------------------------------------- attention

@@ -60,9 +60,9 @@ def test_quantize_rejects_bad_arguments_on_host():
 
 def test_attention_rejects_bad_arguments_on_host():
     lib = _lib.load()
-    args = dict(q=FAKE, batch=1, q_heads=8, kv_heads=2, dim=128, seq=None, n=16, cap=16, kc=FAKE, kn=FAKE,
-                ks=FAKE, kr=FAKE, vc=FAKE, vn=FAKE, kb=3, vb=4, qjl=1, rk=FAKE, ck=FAKE, s=FAKE, rv=FAKE, cv=FAKE,
-                scale=ctypes.c_float(0.0), of=FAKE, ob=FAKE, ws=FAKE, wsb=1 << 30, stream=None)
+    args = dict(q=FAKE, batch=1, q_heads=8, kv_heads=2, dim=128, starts=None, lens=None, n=16, cap=16, kc=FAKE,
+                kn=FAKE, ks=FAKE, kr=FAKE, vc=FAKE, vn=FAKE, kb=3, vb=4, qjl=1, rk=FAKE, ck=FAKE, s=FAKE, rv=FAKE,
+                cv=FAKE, scale=ctypes.c_float(0.0), of=FAKE, ob=FAKE, lse=None, ws=FAKE, wsb=1 << 30, stream=None)
 
     def call(**kw):
         a = dict(args, **kw)

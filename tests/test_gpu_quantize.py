@@ -141,3 +141,22 @@ def test_dequantize_matches_oracle(cuda, bits):
     ref = O.decode_mse(codes[:, :, :200].cpu().numpy().reshape(400, -1), u16(norms[:, :, :200]).reshape(-1),
                        bits, D, R, C)
     assert np.array_equal(u16(out).reshape(400, D), ref)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_dequantize_prod_matches_oracle(cuda, bits):
+    x = kv_bf16((1, 2, 150, D), seed=60 + bits, device=cuda)
+    lc = layer_codecs(D, bits, 0, True, cuda)
+    kb = bits - 1
+    codes = torch.zeros(1, 2, 160, K.row_bytes(D, kb), dtype=torch.uint8, device=cuda)
+    norms = torch.zeros(1, 2, 160, dtype=torch.float16, device=cuda)
+    signs = torch.zeros(1, 2, 160, D // 8, dtype=torch.uint8, device=cuda)
+    rnorms = torch.zeros(1, 2, 160, dtype=torch.float16, device=cuda)
+    K.quantize_prod(x, lc.key, lc.qjl, codes, norms, signs, rnorms)
+    out = K.dequantize_prod(codes, norms, signs, rnorms, 150, lc.key, lc.qjl)
+    torch.cuda.synchronize()
+    R, C, _ = _host(lc.key)
+    ref = O.decode_prod(codes[:, :, :150].cpu().numpy().reshape(300, -1), u16(norms[:, :, :150]).reshape(-1),
+                        signs[:, :, :150].cpu().numpy().reshape(300, -1), u16(rnorms[:, :, :150]).reshape(-1),
+                        kb, D, R, C, lc.qjl.cpu().numpy())
+    assert np.array_equal(u16(out).reshape(300, D), ref)

@@ -111,6 +111,16 @@ def test_oracle_encode_prod_matches_reference(enc):
     assert np.array_equal(O.decode_mse(codes, norms, 3, D, R, c), enc["prod4_khat_bf16"].reshape(-1, D))
 
 
+def test_oracle_decode_prod_matches_reference(enc):
+    """Q_prod key reconstruction (MSE + bf16 QJL correction) equals the reference's
+    _decode_keys_qjl_group output bit for bit."""
+    R, c, _ = _params(3, 1)
+    S = generate_qjl_matrix(D, 31337).numpy()
+    out = O.decode_prod(enc["prod4_codes"].reshape(-1, 48), enc["prod4_norms"].reshape(-1),
+                        enc["prod4_signs"].reshape(-1, 16), enc["prod4_rnorms"].reshape(-1), 3, D, R, c, S)
+    assert np.array_equal(out, enc["prod4_kfull_bf16"].reshape(-1, D))
+
+
 def test_torch_restatement_matches_reference(enc):
     x = torch.from_numpy(enc["x_bf16"].view(np.int16)).view(torch.bfloat16)
     for bits in (2, 3, 4):

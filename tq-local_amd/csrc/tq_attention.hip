@@ -94,7 +94,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int KB, int VB, bool QJL, int G>
 __global__ __launch_bounds__(ABLOCK) void split_kernel(
     const float* __restrict__ qr, const float* __restrict__ qp, int q_heads, int kv_heads,
-    const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
+    const int32_t* __restrict__ seq_starts, const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap,
+    const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
     const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vn, const float* __restrict__ Ck,
     const float* __restrict__ Cv, float scale, int64_t tokens_per_split, int n_split, float* __restrict__ part_o,
@@ -116,8 +117,12 @@ __global__ __launch_bounds__(ABLOCK) void split_kernel(
         const int64_t l = seq_lens[b];
         len = l < n_tokens ? (l < 0 ? 0 : l) : n_tokens;
     }
-    const int64_t t0 = (int64_t)split * tokens_per_split;
+    int64_t t0 = (int64_t)split * tokens_per_split;
     const int64_t t1 = (t0 + tokens_per_split < len) ? t0 + tokens_per_split : len;
+    if (seq_starts) {
+        const int64_t st = seq_starts[b];
+        if (st > t0) t0 = st;
+    }
 
     if (tid < (1 << KB)) sCk[tid] = Ck[tid];
     if (tid < (1 << VB)) sCv[tid] = Cv[tid];
@@ -282,7 +287,8 @@ __global__ __launch_bounds__(ABLOCK) void split_kernel(
 // ----------------------------------------------------------------- merge
 __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                                                   int n_split, const float* __restrict__ Rv,
-                                                  float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16) {
+                                                  float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
+                                                  float* __restrict__ lse_out) {
     __shared__ float so[D];
     const int bh = blockIdx.x, d = threadIdx.x;
     const float* ml = part_ml + (size_t)bh * n_split * 2;
@@ -297,6 +303,7 @@ __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ part
         }
         o = o / fmaxf(sum, 1e-8f);
     }
+    if (lse_out && d == 0) lse_out[bh] = (M != NEG_INF) ? M + logf(sum) : NEG_INF;
     so[d] = o;
     __syncthreads();
     float a = 0.0f;
@@ -308,13 +315,13 @@ __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ part
 
 template <int KB, int VB, bool QJL>
 int launch_split_g(int G, dim3 grid, hipStream_t s, const float* qr, const float* qp, int q_heads, int kv_heads,
-                   const int32_t* seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* kc, const uint16_t* kn,
+                   const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* kc, const uint16_t* kn,
                    const uint8_t* ks, const uint16_t* kr, const uint8_t* vc, const uint16_t* vn, const float* Ck,
                    const float* Cv, float scale, int64_t tps, int n_split, float* po, float* pml) {
 #define TQ_SPLIT(GG)                                                                                           \
     case GG:                                                                                                   \
         hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GG>), grid, dim3(ABLOCK), 0, s, qr, qp, q_heads, kv_heads, \
-                           seq_lens, n_tokens, cap, kc, kn, ks, kr, vc, vn, Ck, Cv, scale, tps, n_split, po, pml); \
+                           seq_starts, seq_lens, n_tokens, cap, kc, kn, ks, kr, vc, vn, Ck, Cv, scale, tps, n_split, po, pml); \
         break;
     switch (G) {
         TQ_SPLIT(1) TQ_SPLIT(2) TQ_SPLIT(3) TQ_SPLIT(4) TQ_SPLIT(5) TQ_SPLIT(6) TQ_SPLIT(7) TQ_SPLIT(8)
@@ -340,12 +347,13 @@ extern "C" size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, in
 }
 
 extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
-                                   const int32_t* seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* k_codes,
+                                   const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
+                                   const uint8_t* k_codes,
                                    const uint16_t* k_norms, const uint8_t* k_signs, const uint16_t* k_rnorms,
                                    const uint8_t* v_codes, const uint16_t* v_norms, int key_bits, int value_bits,
                                    int has_qjl, const float* key_rotation, const float* key_centers,
                                    const float* qjl, const float* value_rotation, const float* value_centers,
-                                   float scale, float* out_f32, uint16_t* out_bf16, void* workspace,
+                                   float scale, float* out_f32, uint16_t* out_bf16, float* lse_out, void* workspace,
                                    size_t workspace_bytes, void* stream) {
     if (!q || batch <= 0 || q_heads <= 0 || kv_heads <= 0 || n_tokens < 0 || cap < n_tokens)
         return TQ_ERR_INVALID_ARGUMENT;
@@ -354,7 +362,7 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     const int G = q_heads / kv_heads;
     if (G > TQ_MAX_GROUP) return TQ_ERR_UNSUPPORTED;
     if (!key_rotation || !key_centers || !value_rotation || !value_centers) return TQ_ERR_INVALID_ARGUMENT;
-    if (!out_f32 && !out_bf16) return TQ_ERR_INVALID_ARGUMENT;
+    if (!out_f32 && !out_bf16 && !lse_out) return TQ_ERR_INVALID_ARGUMENT;
     if (n_tokens > 0 && (!k_codes || !k_norms || !v_codes || !v_norms)) return TQ_ERR_INVALID_ARGUMENT;
     if (has_qjl && (!qjl || (n_tokens > 0 && (!k_signs || !k_rnorms)))) return TQ_ERR_INVALID_ARGUMENT;
     if ((k_codes && !aligned16(k_codes)) || (k_signs && !aligned16(k_signs)) || (v_codes && !aligned16(v_codes)))
@@ -382,22 +390,22 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     int st;
     if (has_qjl) {
         switch (value_bits) {
-            case 2: st = launch_split_g<1, 2, true>(G, grid, s, qr, qp, q_heads, kv_heads, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
-            case 3: st = launch_split_g<2, 3, true>(G, grid, s, qr, qp, q_heads, kv_heads, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
-            default: st = launch_split_g<3, 4, true>(G, grid, s, qr, qp, q_heads, kv_heads, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
+            case 2: st = launch_split_g<1, 2, true>(G, grid, s, qr, qp, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
+            case 3: st = launch_split_g<2, 3, true>(G, grid, s, qr, qp, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
+            default: st = launch_split_g<3, 4, true>(G, grid, s, qr, qp, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
         }
     } else {
         switch (value_bits) {
-            case 1: st = launch_split_g<1, 1, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
-            case 2: st = launch_split_g<2, 2, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
-            case 3: st = launch_split_g<3, 3, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
-            default: st = launch_split_g<4, 4, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
+            case 1: st = launch_split_g<1, 1, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
+            case 2: st = launch_split_g<2, 2, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
+            case 3: st = launch_split_g<3, 3, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
+            default: st = launch_split_g<4, 4, false>(G, grid, s, qr, qp, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms, v_codes, v_norms, key_centers, value_centers, scale, tps, n_split, po, pml); break;
         }
     }
     if (st != TQ_OK) return st;
     TQ_CHECK_LAUNCH();
     hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(D), 0, s, po, pml, n_split, value_rotation, out_f32,
-                       out_bf16);
+                       out_bf16, lse_out);
     TQ_CHECK_LAUNCH();
     return TQ_OK;
 }

@@ -168,13 +168,19 @@ __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
     }
 }
 
-// ------------------------------------------------------------ residual-free decode
-template <int BITS>
+// ------------------------------------------------------------------- dequantise
+// out = bf16((C[code] @ R) * f32(norm)); with QJL (keys of Q_prod) the reference's
+// correction is added in bf16: corr = bf16(((s @ S) * rnorm) * sqrt(pi/2)/D),
+// out = bf16(f32(khat) + f32(corr))   (runtime/packed_qmse_cache.py:312-330, 404-435).
+template <int BITS, bool QJL>
 __global__ __launch_bounds__(QBLOCK) void dequantize_kernel(const uint8_t* __restrict__ codes,
                                                             const uint16_t* __restrict__ norms,
+                                                            const uint8_t* __restrict__ signs,
+                                                            const uint16_t* __restrict__ rnorms,
                                                             int64_t tokens, int64_t cap, int64_t n_vec,
                                                             const float* __restrict__ R,
                                                             const float* __restrict__ centers,
+                                                            const float* __restrict__ S,
                                                             uint16_t* __restrict__ out) {
     __shared__ float s_centers[1 << BITS];
     if (threadIdx.x < (1 << BITS)) s_centers[threadIdx.x] = centers[threadIdx.x];
@@ -198,15 +204,34 @@ __global__ __launch_bounds__(QBLOCK) void dequantize_kernel(const uint8_t* __res
         for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
     }
     const float nf = tq::f16_to_f32(norms[slot]);
+    uint32_t kh[D / 2];  // bf16 pairs
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i)
+        kh[i] = tq::f32_to_bf16(acc[2 * i] * nf) | (tq::f32_to_bf16(acc[2 * i + 1] * nf) << 16);
+    if constexpr (QJL) {
+        const uint8_t* srow = signs + slot * (D / 8);
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        for (int i = 0; i < D; ++i) {
+            const float si = ((srow[i >> 3] >> (i & 7)) & 1u) ? 1.0f : -1.0f;
+            const float* Si = S + i * D;
+#pragma unroll
+            for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(si, Si[d], acc[d]);
+        }
+        const float rn = tq::f16_to_f32(rnorms[slot]);
+        const float qs = 1.2533141373155003f / D;  // sqrt(pi/2)/D rounded to fp32
+#pragma unroll
+        for (int i = 0; i < D / 2; ++i) {
+            const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((acc[2 * i] * rn) * qs));
+            const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((acc[2 * i + 1] * rn) * qs));
+            const float k0 = tq::bf16_to_f32(kh[i] & 0xFFFFu) + c0;
+            const float k1 = tq::bf16_to_f32(kh[i] >> 16) + c1;
+            kh[i] = tq::f32_to_bf16(k0) | (tq::f32_to_bf16(k1) << 16);
+        }
+    }
     uint4* o4 = reinterpret_cast<uint4*>(out + v * D);
 #pragma unroll
-    for (int i = 0; i < D / 8; ++i) {
-        uint32_t p[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            p[k] = tq::f32_to_bf16(acc[8 * i + 2 * k] * nf) | (tq::f32_to_bf16(acc[8 * i + 2 * k + 1] * nf) << 16);
-        o4[i] = make_uint4(p[0], p[1], p[2], p[3]);
-    }
+    for (int i = 0; i < D / 8; ++i) o4[i] = make_uint4(kh[4 * i], kh[4 * i + 1], kh[4 * i + 2], kh[4 * i + 3]);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -274,11 +299,15 @@ extern "C" int tq_quantize_prod(const uint16_t* x, int batch, int heads, int64_t
     }
 }
 
-extern "C" int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, int64_t groups, int64_t tokens,
-                                 int64_t cap, int dim, int bits, const float* rotation, const float* centers,
-                                 uint16_t* out, void* stream) {
+namespace {
+
+template <bool QJL>
+int launch_dequantize(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs, const uint16_t* rnorms,
+                      int64_t groups, int64_t tokens, int64_t cap, int dim, int bits, const float* rotation,
+                      const float* centers, const float* qjl, uint16_t* out, void* stream) {
     if (!codes || !norms || !rotation || !centers || !out || groups < 0 || tokens < 0 || tokens > cap)
         return TQ_ERR_INVALID_ARGUMENT;
+    if (QJL && (!signs || !rnorms || !qjl)) return TQ_ERR_INVALID_ARGUMENT;
     if (dim != TQ_DIM) return TQ_ERR_UNSUPPORTED;
     if (!aligned16(codes) || !aligned16(out)) return TQ_ERR_UNSUPPORTED;
     const int64_t n_vec = groups * tokens;
@@ -286,10 +315,10 @@ extern "C" int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, in
     if (blocks == 0) return TQ_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (bits) {
-#define TQ_DQ(B)                                                                                          \
-    case B:                                                                                               \
-        hipLaunchKernelGGL(dequantize_kernel<B>, dim3((unsigned)blocks), dim3(QBLOCK), 0, s, codes, norms, \
-                           tokens, cap, n_vec, rotation, centers, out);                                   \
+#define TQ_DQ(B)                                                                                             \
+    case B:                                                                                                  \
+        hipLaunchKernelGGL((dequantize_kernel<B, QJL>), dim3((unsigned)blocks), dim3(QBLOCK), 0, s, codes, norms, \
+                           signs, rnorms, tokens, cap, n_vec, rotation, centers, qjl, out);                    \
         break;
         TQ_DQ(1) TQ_DQ(2) TQ_DQ(3) TQ_DQ(4)
 #undef TQ_DQ
@@ -297,4 +326,22 @@ extern "C" int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, in
     }
     TQ_CHECK_LAUNCH();
     return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, int64_t groups, int64_t tokens,
+                                 int64_t cap, int dim, int bits, const float* rotation, const float* centers,
+                                 uint16_t* out, void* stream) {
+    return launch_dequantize<false>(codes, norms, nullptr, nullptr, groups, tokens, cap, dim, bits, rotation,
+                                    centers, nullptr, out, stream);
+}
+
+extern "C" int tq_dequantize_prod(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
+                                  const uint16_t* rnorms, int64_t groups, int64_t tokens, int64_t cap, int dim,
+                                  int mse_bits, const float* rotation, const float* centers, const float* qjl,
+                                  uint16_t* out, void* stream) {
+    if (mse_bits > 3) return TQ_ERR_INVALID_ARGUMENT;
+    return launch_dequantize<true>(codes, norms, signs, rnorms, groups, tokens, cap, dim, mse_bits, rotation,
+                                   centers, qjl, out, stream);
 }

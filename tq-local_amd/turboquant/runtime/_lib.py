@@ -30,9 +30,10 @@ SIGNATURES: dict[str, tuple] = {
     "tq_quantize_prod": (_I, [_P, _I, _I, _I64, _I, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                               _I64, _I64, _P]),
     "tq_decode_attention_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I64]),
-    "tq_decode_attention": (_I, [_P, _I, _I, _I, _I, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I, _I, _I,
-                                 _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _P]),
+    "tq_decode_attention": (_I, [_P, _I, _I, _I, _I, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                 _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _SZ, _P]),
     "tq_dequantize_mse": (_I, [_P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
+    "tq_dequantize_prod": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

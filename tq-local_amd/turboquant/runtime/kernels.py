@@ -110,6 +110,17 @@ def dequantize_mse(codes: torch.Tensor, norms: torch.Tensor, tokens: int, codec:
     return out
 
 
+def dequantize_prod(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Tensor, rnorms: torch.Tensor,
+                    tokens: int, codec: CodecParams, qjl: torch.Tensor, dim: int = HEAD_DIM) -> torch.Tensor:
+    """Q_prod keys [B,H,cap,...] -> bf16 [B,H,tokens,D]: MSE reconstruction + QJL correction."""
+    _require_gpu(codes, norms, signs, rnorms)
+    B, H, cap, _ = codes.shape
+    out = torch.empty(B, H, tokens, dim, dtype=torch.bfloat16, device=codes.device)
+    _lib.call("tq_dequantize_prod", _vp(codes), _vp(norms), _vp(signs), _vp(rnorms), B * H, tokens, cap, dim,
+              codec.bits, _vp(codec.rotation), _vp(codec.centers), _vp(qjl), _vp(out), _stream(codes.device))
+    return out
+
+
 _workspaces: dict[tuple, torch.Tensor] = {}
 
 
@@ -129,12 +140,15 @@ def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.T
                      v_norms: torch.Tensor, n_tokens: int, key: CodecParams, value: CodecParams,
                      k_signs: torch.Tensor | None = None, k_rnorms: torch.Tensor | None = None,
                      qjl: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None,
-                     scale: float | None = None, want_f32: bool = False):
+                     seq_starts: torch.Tensor | None = None, scale: float | None = None,
+                     want_f32: bool = False, want_lse: bool = False):
     """Fused decode attention for one query token per sequence.
 
     q: [B, Hq, D] or [B, Hq, 1, D] (any float dtype; bf16 is passed through).
-    Packed buffers are [B, Hkv, cap, ...] with ``n_tokens`` valid slots.
-    Returns bf16 [B, Hq, D] (and fp32 [B, Hq, D] if ``want_f32``).
+    Packed buffers are [B, Hkv, cap, ...] with ``n_tokens`` valid slots; row b
+    attends to slots [seq_starts[b], seq_lens[b]) when those are given.
+    Returns bf16 [B, Hq, D], then fp32 [B, Hq, D] if ``want_f32`` and the fp32
+    log-sum-exp [B, Hq] of the scaled logits if ``want_lse``.
     """
     if q.dim() == 4:
         if q.shape[2] != 1:
@@ -148,12 +162,16 @@ def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.T
     out_bf16 = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=q.device)
     out_f32 = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device) if want_f32 else None
     ws = attention_workspace(q.device, B, Hq, Hkv, max(int(n_tokens), 1))
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=q.device) if want_lse else None
     if seq_lens is not None:
         seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
+    if seq_starts is not None:
+        seq_starts = seq_starts.to(device=q.device, dtype=torch.int32).contiguous()
     s = float(scale) if scale is not None else 1.0 / math.sqrt(D)
-    _lib.call("tq_decode_attention", _vp(q), B, Hq, Hkv, D, _vp(seq_lens), int(n_tokens), cap,
+    _lib.call("tq_decode_attention", _vp(q), B, Hq, Hkv, D, _vp(seq_starts), _vp(seq_lens), int(n_tokens), cap,
               _vp(k_codes), _vp(k_norms), _vp(k_signs), _vp(k_rnorms), _vp(v_codes), _vp(v_norms),
               key.bits, value.bits, int(has_qjl), _vp(key.rotation), _vp(key.centers), _vp(qjl),
               _vp(value.rotation), _vp(value.centers), ctypes.c_float(s), _vp(out_f32), _vp(out_bf16),
-              _vp(ws), ws.numel(), _stream(q.device))
-    return (out_bf16, out_f32) if want_f32 else out_bf16
+              _vp(lse), _vp(ws), ws.numel(), _stream(q.device))
+    outs = (out_bf16,) + ((out_f32,) if want_f32 else ()) + ((lse,) if want_lse else ())
+    return outs if len(outs) > 1 else out_bf16

@@ -1,0 +1,417 @@
+"""Packed TurboQuant KV cache (a transformers ``CacheLayerMixin``) backed by libtq.
+
+Drop-in for reference ``runtime/packed_qmse_cache.py``: the same container
+types (``PackedTensorMSE``, ``PackedQJL``), the same per-layer attribute names
+(``keys_packed``, ``_keys_qjl``, ``values_packed``, ``_dense_keys``, ...), the
+same packed layout, seed schedule, norm guard and reconstruction report.
+
+Differences, all on purpose:
+* Storage is capacity-preallocated ``[B, H, cap, row]`` buffers; decode-append
+  encodes the new token straight into slot ``N`` (one kernel launch per tensor)
+  instead of the reference's ``torch.cat`` of the whole history
+  (``runtime/packed_qmse_cache.py:81-92, 135-140``).  ``keys_packed`` etc. are
+  ``[:, :, :N]`` views of those buffers.
+* Every encode / decode is a libtq HIP kernel; there is no CPU path.
+* ``get_mask_sizes(query_length)`` / ``get_max_length()`` follow the installed
+  transformers (5.x) cache-layer protocol.
+* The outlier-channel split (``num_outlier_channels > 0``) is not implemented:
+  it is off by default in the reference and its fused path refuses it.
+"""
+
+from __future__ import annotations
+
+import sys
+from dataclasses import dataclass
+from math import sqrt
+from typing import Any
+
+import torch
+from transformers.cache_utils import Cache, CacheLayerMixin
+
+from turboquant.runtime import kernels as K
+from turboquant.runtime.params import LayerCodecs, layer_codecs
+
+#: growth step of the capacity buffers when decode-append runs out of slots
+DEFAULT_RESERVE_TOKENS = 256
+
+
+@dataclass
+class PackedTensorMSE:
+    """Packed Q_mse codes of one tensor [B, H, N, D] (reference :58-92)."""
+
+    packed_indices: torch.Tensor  # u8 [B, H, N, ceil(D*bits/8)]
+    norms: torch.Tensor  # f16 [B, H, N]
+    original_shape: tuple[int, int, int, int]
+    original_dtype: torch.dtype
+    bits: int
+
+    @property
+    def num_vectors(self) -> int:
+        b, h, n, _ = self.original_shape
+        return int(b * h * n)
+
+    @property
+    def dimension(self) -> int:
+        return int(self.original_shape[-1])
+
+    def storage_bytes(self) -> int:
+        return int(self.packed_indices.numel() * self.packed_indices.element_size()
+                   + self.norms.numel() * self.norms.element_size())
+
+
+@dataclass
+class PackedQJL:
+    """1-bit QJL sign sketch and residual norms (reference :121-140)."""
+
+    packed_signs: torch.Tensor  # u8 [B, H, N, D/8]
+    residual_norms: torch.Tensor  # f16 [B, H, N]
+    dimension: int
+
+    def storage_bytes(self) -> int:
+        return int(self.packed_signs.numel() * self.packed_signs.element_size()
+                   + self.residual_norms.numel() * self.residual_norms.element_size())
+
+
+class _Store:
+    """Capacity buffers of one packed layer; slots [0, length) are valid."""
+
+    def __init__(self, B: int, H: int, D: int, cap: int, codecs: LayerCodecs, device: torch.device):
+        self.B, self.H, self.D, self.codecs, self.device = B, H, D, codecs, device
+        self.length = 0
+        self.cap = 0
+        self.kc = self.kn = self.ks = self.kr = self.vc = self.vn = None
+        self._alloc(cap)
+
+    def _alloc(self, cap: int) -> None:
+        B, H, D, c = self.B, self.H, self.D, self.codecs
+        dev = self.device
+        new = {
+            "kc": torch.zeros(B, H, cap, K.row_bytes(D, c.key_bits), dtype=torch.uint8, device=dev),
+            "kn": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
+            "vc": torch.zeros(B, H, cap, K.row_bytes(D, c.value_bits), dtype=torch.uint8, device=dev),
+            "vn": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
+            "ks": torch.zeros(B, H, cap, D // 8, dtype=torch.uint8, device=dev) if c.use_qjl_keys else None,
+            "kr": torch.zeros(B, H, cap, dtype=torch.float16, device=dev) if c.use_qjl_keys else None,
+        }
+        n = self.length
+        for name, buf in new.items():
+            old = getattr(self, name)
+            if buf is not None and old is not None and n:
+                buf[:, :, :n].copy_(old[:, :, :n])
+            setattr(self, name, buf)
+        self.cap = cap
+
+    def reserve(self, extra: int, reserve_tokens: int) -> None:
+        need = self.length + extra
+        if need > self.cap:
+            self._alloc(max(need + reserve_tokens, 2 * self.cap))
+
+    def append(self, k: torch.Tensor, v: torch.Tensor, reserve_tokens: int) -> None:
+        T = int(k.shape[2])
+        self.reserve(T, reserve_tokens)
+        c = self.codecs
+        if c.use_qjl_keys:
+            K.quantize_prod(k, c.key, c.qjl, self.kc, self.kn, self.ks, self.kr, offset=self.length)
+        else:
+            K.quantize_mse(k, c.key, self.kc, self.kn, offset=self.length)
+        K.quantize_mse(v, c.value, self.vc, self.vn, offset=self.length)
+        self.length += T
+
+
+class PackedMSELayer(CacheLayerMixin):
+    """One decoder layer's TurboQuant-compressed KV cache."""
+
+    is_sliding = False
+    is_compileable = False
+
+    def __init__(self, bits: int, seed: int = 0, grid_size: int = 32769, num_outlier_channels: int = 0,
+                 outlier_extra_bits: int = 1, use_qjl_keys: bool = False, quantize_decode: bool = False,
+                 reserve_tokens: int = DEFAULT_RESERVE_TOKENS):
+        super().__init__()
+        if num_outlier_channels:
+            raise NotImplementedError("the outlier-channel split (num_outlier_channels > 0) is not supported "
+                                      "by the MI355X TurboQuant path")
+        self.bits = bits
+        self.seed = seed
+        self.grid_size = grid_size
+        self.num_outlier_channels = num_outlier_channels
+        self.outlier_extra_bits = outlier_extra_bits
+        self.use_qjl_keys = use_qjl_keys
+        self.quantize_decode = quantize_decode
+        self.reserve_tokens = reserve_tokens
+        self.device: torch.device | None = None
+        self.dtype: torch.dtype | None = None
+        self.codecs: LayerCodecs | None = None
+        self._store: _Store | None = None
+        self._shape: tuple[int, int, int] | None = None  # (B, H, D)
+        self._force_dense = False
+        self._lazy_update = False
+        self._dense_keys: torch.Tensor | None = None
+        self._dense_values: torch.Tensor | None = None
+
+    # ------------------------------------------------------------- parameters
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        self.dtype = key_states.dtype
+        self.device = key_states.device
+        self.codecs = layer_codecs(int(key_states.shape[-1]), self.bits, self.seed, self.use_qjl_keys, self.device,
+                                   self.grid_size)
+        self.is_initialized = True
+
+    # reference-compatible parameter attributes
+    @property
+    def rotation(self):
+        return None if self.codecs is None else self.codecs.value.rotation
+
+    @property
+    def centers(self):
+        return None if self.codecs is None else self.codecs.value.centers
+
+    @property
+    def boundaries(self):
+        return None if self.codecs is None else self.codecs.value.boundaries
+
+    @property
+    def _key_rotation(self):
+        return None if self.codecs is None else self.codecs.key.rotation
+
+    @property
+    def _key_centers(self):
+        return None if self.codecs is None else self.codecs.key.centers
+
+    @property
+    def _key_boundaries(self):
+        return None if self.codecs is None else self.codecs.key.boundaries
+
+    @property
+    def _qjl_matrix(self):
+        return None if self.codecs is None else self.codecs.qjl
+
+    @property
+    def _outlier_enabled(self) -> bool:
+        return False
+
+    # ---------------------------------------------------------- packed views
+    def packed_seq_length(self) -> int:
+        return 0 if self._store is None else self._store.length
+
+    def _view_shape(self) -> tuple[int, int, int, int]:
+        B, H, D = self._shape
+        return (B, H, self.packed_seq_length(), D)
+
+    @property
+    def keys_packed(self) -> PackedTensorMSE | None:
+        s = self._store
+        if s is None:
+            return None
+        n = s.length
+        return PackedTensorMSE(s.kc[:, :, :n], s.kn[:, :, :n], self._view_shape(), self.dtype, self.codecs.key_bits)
+
+    @property
+    def values_packed(self) -> PackedTensorMSE | None:
+        s = self._store
+        if s is None:
+            return None
+        n = s.length
+        return PackedTensorMSE(s.vc[:, :, :n], s.vn[:, :, :n], self._view_shape(), self.dtype, self.codecs.value_bits)
+
+    @property
+    def _keys_qjl(self) -> PackedQJL | None:
+        s = self._store
+        if s is None or not self.use_qjl_keys:
+            return None
+        n = s.length
+        return PackedQJL(s.ks[:, :, :n], s.kr[:, :, :n], self._shape[2])
+
+    # ------------------------------------------------------------- encoding
+    def initialize_from_dense(self, key_states: torch.Tensor, value_states: torch.Tensor, *,
+                              force_dense: bool = False) -> None:
+        """Prefill: compress the whole dense K/V (reference :332-374)."""
+        if force_dense:
+            self.device, self.dtype = key_states.device, key_states.dtype
+            self._dense_keys, self._dense_values = key_states, value_states
+            self._force_dense = True
+            self.is_initialized = True
+            return
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        self._append_packed(key_states, value_states)
+
+    def _append_packed(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        B, H, T, D = key_states.shape
+        if self._store is None:
+            self._shape = (int(B), int(H), int(D))
+            self._store = _Store(int(B), int(H), int(D), max(int(T) + self.reserve_tokens, 1), self.codecs,
+                                 key_states.device)
+        elif (int(B), int(H), int(D)) != self._shape:
+            raise ValueError(f"append of shape {tuple(key_states.shape)} to a cache of {self._shape}")
+        self._store.append(key_states, value_states, self.reserve_tokens)
+
+    # ------------------------------------------------------------- decoding
+    def _decode_keys_full(self) -> torch.Tensor | None:
+        s = self._store
+        if s is None:
+            return None
+        c = self.codecs
+        if c.use_qjl_keys:
+            return K.dequantize_prod(s.kc, s.kn, s.ks, s.kr, s.length, c.key, c.qjl).to(self.dtype)
+        return K.dequantize_mse(s.kc, s.kn, s.length, c.key).to(self.dtype)
+
+    def _decode_values_full(self) -> torch.Tensor | None:
+        s = self._store
+        if s is None:
+            return None
+        return K.dequantize_mse(s.vc, s.vn, s.length, self.codecs.value).to(self.dtype)
+
+    # ------------------------------------------------------------ HF protocol
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args: Any,
+               **kwargs: Any) -> tuple[torch.Tensor, torch.Tensor]:
+        """Reference :600-624.  With the TurboQuant attention backend wired
+        (``_lazy_update``) only the new token is stored and returned; otherwise
+        the decoded history plus the new tokens is returned for dense attention."""
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        if self._lazy_update and not self._force_dense:
+            return self._update_lazy(key_states, value_states)
+        if self._force_dense or not self.quantize_decode:
+            return self._update_dense_decode(key_states, value_states)
+        prev_k = self._decode_keys_full()
+        prev_v = self._decode_values_full()
+        self._append_packed(key_states, value_states)
+        if prev_k is None:
+            return key_states, value_states
+        return torch.cat((prev_k, key_states), dim=-2), torch.cat((prev_v, value_states), dim=-2)
+
+    def _update_lazy(self, key_states: torch.Tensor, value_states: torch.Tensor):
+        """Reference :626-679: store the new token without touching the history."""
+        if self.quantize_decode:
+            self._append_packed(key_states, value_states)
+        else:
+            self._append_dense(key_states, value_states)
+        return key_states, value_states
+
+    def _append_dense(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        if self._dense_keys is None:
+            self._dense_keys, self._dense_values = key_states, value_states
+        else:
+            self._dense_keys = torch.cat((self._dense_keys, key_states), dim=-2)
+            self._dense_values = torch.cat((self._dense_values, value_states), dim=-2)
+
+    def _update_dense_decode(self, key_states: torch.Tensor, value_states: torch.Tensor):
+        """Reference :681-705: generated tokens stay dense; history is decoded."""
+        pk, pv = self._decode_keys_full(), self._decode_values_full()
+        self._append_dense(key_states, value_states)
+        ks = [t for t in (pk, self._dense_keys) if t is not None]
+        vs = [t for t in (pv, self._dense_values) if t is not None]
+        return torch.cat(ks, dim=-2), torch.cat(vs, dim=-2)
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        if torch.is_tensor(query_length):  # older callers pass cache_position
+            query_length = int(query_length.shape[0])
+        return self.get_seq_length() + int(query_length), 0
+
+    def get_seq_length(self) -> int:
+        dense = 0 if self._dense_keys is None else int(self._dense_keys.shape[-2])
+        return self.packed_seq_length() + dense
+
+    def get_max_length(self) -> int:
+        return -1
+
+    def get_max_cache_shape(self) -> int:
+        return -1
+
+    def storage_bytes(self) -> int:
+        """Logical storage (N valid tokens, as the reference counts it; :874-885)."""
+        total = 0
+        for p in (self.keys_packed, self.values_packed, self._keys_qjl):
+            if p is not None:
+                total += p.storage_bytes()
+        for d in (self._dense_keys, self._dense_values):
+            if d is not None:
+                total += d.numel() * d.element_size()
+        return int(total)
+
+
+_APPROX_DMSE_UNIT: dict[int, float] = {2: 0.079, 3: 0.030, 4: 0.009, 5: 0.003, 6: 0.0008, 7: 0.0002, 8: 0.00005}
+
+
+def _auto_norm_threshold(bits: int, head_dim: int, mse_budget: float = 1.0) -> float:
+    """Largest mean key norm a layer may have before the norm guard keeps it dense
+    (reference :888-900): norm^2 * D_mse(bits) / D < budget."""
+    return sqrt(mse_budget * head_dim / _APPROX_DMSE_UNIT.get(bits, 0.03))
+
+
+def _layer_kv(past_key_values):
+    if hasattr(past_key_values, "layers"):
+        return [(layer.keys, layer.values) for layer in past_key_values.layers]
+    return [(k, v) for k, v, *_ in past_key_values]
+
+
+def build_packed_mse_cache(past_key_values, bits: int, seed: int = 0, grid_size: int = 32769,
+                           num_outlier_channels: int = 0, outlier_extra_bits: int = 1, use_qjl_keys: bool = False,
+                           quantize_decode: bool = False, norm_guard: bool = True,
+                           reserve_tokens: int = DEFAULT_RESERVE_TOKENS) -> Cache:
+    """Compress a prefilled dense cache layer by layer (reference :903-951)."""
+    data = _layer_kv(past_key_values)
+    if not data:
+        return Cache(layers=[])
+    # one host sync for all layers' mean key norms (reference: one .item() per layer)
+    norms = torch.stack([k.float().norm(dim=-1).mean().to(data[0][0].device) for k, _ in data]).tolist()
+    head_dim = int(data[0][0].shape[-1])
+    threshold = _auto_norm_threshold(bits, head_dim) if norm_guard else float("inf")
+    layers = []
+    for (k, v), n in zip(data, norms):
+        layer = PackedMSELayer(bits=bits, seed=seed, grid_size=grid_size, num_outlier_channels=num_outlier_channels,
+                               outlier_extra_bits=outlier_extra_bits, use_qjl_keys=use_qjl_keys,
+                               quantize_decode=quantize_decode, reserve_tokens=reserve_tokens)
+        layer.initialize_from_dense(k, v, force_dense=n > threshold)
+        layers.append(layer)
+    dense_ids = [i for i, n in enumerate(norms) if n > threshold]
+    if dense_ids:
+        print(f"[TurboQuant] norm_guard: {len(dense_ids)}/{len(layers)} layers kept dense "
+              f"(threshold={threshold:.1f}, layers={dense_ids})", file=sys.stderr)
+    return Cache(layers=layers)
+
+
+def verify_packed_reconstruction(original_cache, packed_cache: Cache) -> list[dict[str, Any]]:
+    """Per-layer reconstruction quality of the packed cache (reference :954-1009)."""
+    out: list[dict[str, Any]] = []
+    for idx, (ko, vo) in enumerate(_layer_kv(original_cache)):
+        layer: PackedMSELayer = packed_cache.layers[idx]
+        kr, vr = layer._decode_keys_full(), layer._decode_values_full()
+        dense = kr is None and layer._dense_keys is not None
+        if dense:
+            kr, vr = layer._dense_keys, layer._dense_values
+        ko32, kr32, vo32, vr32 = ko.float(), kr.float(), vo.float(), vr.float()
+        ke, ve = ko32 - kr32, vo32 - vr32
+        D = ko32.shape[-1]
+        stats = torch.stack([
+            (ke ** 2).mean(),
+            torch.nn.functional.cosine_similarity(ko32.reshape(-1, D), kr32.reshape(-1, D), dim=-1).mean(),
+            ke.abs().max(),
+            ko32.norm(dim=-1).mean(),
+            (ve ** 2).mean(),
+            torch.nn.functional.cosine_similarity(vo32.reshape(-1, D), vr32.reshape(-1, D), dim=-1).mean(),
+            ve.abs().max(),
+            vo32.norm(dim=-1).mean(),
+        ]).tolist()
+        out.append({
+            "layer": idx, "dense": dense,
+            "key_mse": round(stats[0], 6), "key_cosine_sim": round(stats[1], 6),
+            "key_max_abs_error": round(stats[2], 6), "key_mean_norm": round(stats[3], 4),
+            "val_mse": round(stats[4], 6), "val_cosine_sim": round(stats[5], 6),
+            "val_max_abs_error": round(stats[6], 6), "val_mean_norm": round(stats[7], 4),
+        })
+    return out
+
+
+def packed_cache_storage_bytes(cache: Cache) -> int:
+    return sum(int(layer.storage_bytes()) for layer in cache.layers if hasattr(layer, "storage_bytes"))
+
+
+def packed_cache_storage_breakdown(cache: Cache) -> dict[str, int]:
+    sizes = [int(layer.storage_bytes()) for layer in cache.layers if hasattr(layer, "storage_bytes")]
+    return {
+        "packed_total_bytes": int(sum(sizes)),
+        "packed_layer_mean_bytes": int(sum(sizes) / len(sizes)) if sizes else 0,
+        "packed_num_layers": len(sizes),
+    }
