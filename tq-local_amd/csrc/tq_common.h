@@ -38,13 +38,13 @@ __device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, 
 __device__ __forceinline__ float sqrt_rn(float a) { return __fsqrt_rn(a); }
 
 // Bits [pos, pos+n) of a little-endian word array held in registers, pos and
-// n compile-time constants after unrolling.
+// n compile-time constants after unrolling: one v_bfe_u32, plus a v_alignbit_b32
+// when the field straddles two words.
 template <int N>
 __device__ __forceinline__ uint32_t extract_bits(const uint32_t* w, int pos) {
     const int wi = pos >> 5, sh = pos & 31;
-    uint32_t v = w[wi] >> sh;
-    if (sh + N > 32) v |= w[wi + 1] << (32 - sh);
-    return v & ((1u << N) - 1u);
+    if (sh + N > 32) return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh), 0, N);
+    return __builtin_amdgcn_ubfe(w[wi], sh, N);
 }
 
 }  // namespace tq
