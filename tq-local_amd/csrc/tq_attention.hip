@@ -2,76 +2,108 @@
 //
 // Two launches per call, on the caller's stream:
 //
-//   split_kernel  grid (n_split, batch * kv_heads), 4 waves per workgroup.  One
+//   split_kernel  grid (n_split, batch * kv_heads), NW waves per workgroup.  A
 //                 workgroup owns a contiguous token range of one (batch row, KV
-//                 head); all G query heads of the GQA group share every K/V byte
-//                 it reads (reference runtime/triton_kernels.py:84-198, which
+//                 head); each wave owns a contiguous sub-range and walks it in
+//                 blocks of 16 tokens.  All G query heads of the GQA group share
+//                 every K/V byte read (reference runtime/triton_kernels.py:84-198
 //                 re-reads the tile once per query head).
-//     prologue    q_rot = q @ R_k^T, q_proj = q @ S^T for the G heads (reference
-//                 :289, 305-306); a byte-indexed QJL table
-//                 T[pos][byte] = sum_{bit i of byte} q_proj[8 pos + i] (one float per
-//                 head); pair tables of codebook values for K and V.
-//     key pass    per 16 tokens: lane (token, 32-dim group) unpacks its codes two at
-//                 a time through the K pair table and feeds them as the B operand of
-//                 v_mfma_f32_4x4x1_16b_f32 (16 independent 4x4 blocks: M = 4 query
-//                 heads, N = 4 tokens, K = 1 dim); A is q_rot, held in VGPRs.  The
-//                 QJL term is four byte-table lookups.  Group partials are summed
-//                 with DPP row rotations.
-//     softmax     online, per 64-token tile, max tracked per head.
-//     value pass  per 4 tokens: lane (token, 8 dims) unpacks codes through the V
-//                 pair table into the B operand; A = p * |v| per head; 8 MFMA chains
-//                 (one per dim of the lane's 8) accumulate sum_t w C_v[code].
-//     epilogue    waves merge by log-sum-exp in LDS; one (o[D], max, sum) partial
-//                 per (query head, split) is written.
 //   merge_kernel  log-sum-exp merge over splits, normalise, un-rotate by R_v, write
 //                 fp32 / bf16 / lse (reference :330-336, 366-368).
 //
-// Everything accumulates in fp32 (MFMA f32, VALU f32); no packed-fp32 VALU ops.
+// Per 16-token block, lane l = (n = l & 15, g = l >> 4):
+//
+//   key score     v_mfma_f32_16x16x32_bf16, D[row][token] += A[row][k] B[k][token].
+//                 A (registers, fixed for the call): rows = (query head, hi|lo part of
+//                 q_rot = q R_k^T in bf16), k-slots = (dim, hi|lo part of the codebook
+//                 value); B = the dequantised keys, one 8-byte LDS lookup per pair of
+//                 codes returning (Ck_hi, Ck_lo) for both.  Every cross product of the
+//                 two-term splits is formed, so the score carries ~2^-17 relative error
+//                 against fp32 inputs (the fp32 reference rounds at 2^-24; the
+//                 tolerance is 2e-3 of |out|).
+//   QJL term      v_mfma_i32_16x16x64_i8 on the raw sign bits (bytes of 0/1, two VALU
+//                 ops per 4 dims) against q_proj = q S^T in 32-bit fixed point split in
+//                 four int8 limbs (rows = (head, limb)); exact integer accumulation.
+//   softmax       online, base 2 (scores are pre-multiplied by log2 e), per head.
+//   value sum     v_mfma_f32_16x16x32_bf16, D[(head, w hi|lo)][dim] += A B: A = the
+//                 softmax weights p |v| split hi/lo, transposed through LDS; B = value
+//                 codes dequantised by single-code LDS lookups (Cv_hi, Cv_lo) from a
+//                 table small enough to be bank-conflict free.
+//
+// Everything accumulates in fp32 (MFMA f32 / i32 accumulators); no packed-fp32 VALU.
 
 #include "tq_common.h"
 
 namespace {
 
 constexpr int D = TQ_DIM;
-constexpr int NWAVE = 4;
-constexpr int NT = NWAVE * 64;  // threads of a split workgroup
-constexpr int MIN_WAVES_PER_SIMD = 2;
-constexpr int TILE = 64;        // tokens per wave iteration
-constexpr int TARGET_WGS = 512; // two resident 8-wave workgroups on each of 256 CUs
+constexpr int NW = 8;          // waves per split workgroup
+constexpr int NT = NW * 64;    // threads per split workgroup
+constexpr int BLK = 16;        // tokens per block (MFMA N)
+constexpr int WT_STRIDE = 20;  // dwords per row of the weight-transpose buffer (bank spread)
 constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
 constexpr float QJL_SCALE = 1.2533141373155003f / D;  // sqrt(pi/2) / D
 
-typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ f4 mfma4x4(float a, float b, f4 c) {
-    return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+__device__ __forceinline__ i32x4 mfma_i8(const u32x4& a, const u32x4& b, i32x4 c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
+                                                 0);
+}
+
+// bf16 (round to nearest even) of x and of the remainder x - bf16(x): x = hi + lo to ~2^-17.
+__device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo) {
+    hi = tq::f32_to_bf16(x);
+    lo = tq::f32_to_bf16(x - tq::bf16_to_f32(hi));
+}
+__device__ __forceinline__ uint32_t pack_hilo(float x) {
+    uint32_t hi, lo;
+    split_bf16(x, hi, lo);
+    return hi | (lo << 16);
 }
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-constexpr int DPP_QUAD_XOR1 = 0xB1;  // quad_perm [1,0,3,2]
-constexpr int DPP_QUAD_XOR2 = 0x4E;  // quad_perm [2,3,0,1]
-constexpr int DPP_ROR4 = 0x124;      // row_ror:4
-constexpr int DPP_ROR8 = 0x128;      // row_ror:8
+constexpr int DPP_QUAD_XOR1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // row_half_mirror (lane i <-> 7 - i within 8)
+constexpr int DPP_MIRROR = 0x140;       // row_mirror (lane i <-> 15 - i within 16)
 
-__device__ __forceinline__ float swz_xor16(float v) {  // lane ^ 16 within each half-wave
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
-}
-
-// max over the 16 lanes that differ in bits {0,1,4,5} of the lane id, result uniform
-__device__ __forceinline__ float max_tokens(float v) {
+// max / sum over the 16 lanes of a row, result in every lane of the row
+__device__ __forceinline__ float row_max16(float v) {
     v = fmaxf(v, dpp<DPP_QUAD_XOR1>(v));
     v = fmaxf(v, dpp<DPP_QUAD_XOR2>(v));
-    v = fmaxf(v, swz_xor16(v));
-    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    return fmaxf(a, b);
+    v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+    return fmaxf(v, dpp<DPP_MIRROR>(v));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp<DPP_QUAD_XOR1>(v);
+    v += dpp<DPP_QUAD_XOR2>(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    return v + dpp<DPP_MIRROR>(v);
 }
 
-__device__ __forceinline__ float sel4(const f4& v, int i) {
-    return i == 0 ? v[0] : (i == 1 ? v[1] : (i == 2 ? v[2] : v[3]));
+// Bits [pos, pos + N) of a little-endian word array held in registers, returned
+// shifted left by S (an LDS byte offset into a table of 2^S-byte entries).  pos, N
+// and S are compile-time constants after unrolling: two VALU ops per field.
+template <int N, int S>
+__device__ __forceinline__ uint32_t field_x(const uint32_t* w, int pos) {
+    const int wi = pos >> 5, sh = pos & 31;
+    constexpr uint32_t M = ((1u << N) - 1u) << S;
+    if (sh + N > 32) return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - S) & M;
+    if (sh >= S) return (w[wi] >> (sh - S)) & M;
+    return (w[wi] << (S - sh)) & M;
 }
 
 struct Ws {
@@ -89,150 +121,181 @@ Ws ws_layout(int batch, int q_heads, int n_split) {
     return w;
 }
 
-int choose_split(int groups, int64_t n_tokens, int64_t* tokens_per_split) {
-    const int64_t unit = NWAVE * TILE;
-    const int64_t max_split = (n_tokens + unit - 1) / unit;
-    const int64_t want = (TARGET_WGS + groups - 1) / groups;
-    int64_t n_split = want < max_split ? want : max_split;
-    if (n_split < 1) n_split = 1;
-    int64_t per = (n_tokens + n_split - 1) / n_split;
-    per = (per + unit - 1) / unit * unit;
-    if (per < unit) per = unit;
-    *tokens_per_split = per;
-    const int64_t n = (n_tokens + per - 1) / per;
-    return (int)(n > 0 ? n : 1);
-}
+// Upper bound on splits per group for any token count: the grid never exceeds
+// MAX_RESIDENT_WGS workgroups (more would queue behind the first wave of them).
+constexpr int MAX_RESIDENT_WGS = 256 * 4;
 
 // ------------------------------------------------------------------ split kernel
-template <int KB, int VB, bool QJL, int G>
-struct SplitSmem {
-    static constexpr int NQ = (G + 3) / 4;
-    static constexpr int NH = NQ * 4;
-    // the small tables come first so their LDS offsets fit the DS immediate field
-    float2 lutk[1 << (2 * KB)];        // (C_k[lo], C_k[hi]) per pair of key codes
-    float2 lutv[1 << (2 * VB)];        // (C_v[lo], C_v[hi]) per pair of value codes
-    f4 lutq[QJL ? NQ * 16 * 256 : 1];  // QJL byte table, 4 heads per entry
+// GC = 1: at most 4 query heads per KV head; row 4h + x of every MFMA belongs to
+//         head h, so lane group g (lanes 16g..16g+15) holds head g everywhere.
+// GC = 2: 5..8 heads; rows 2h + x, lane group g holds heads 2g and 2g + 1.
+template <int GC>
+struct Rows {
+    static constexpr int HPL = GC;      // heads per lane group
+    static constexpr int NQJ = GC;      // QJL MFMA sets (4 limbs per head in total)
+    __host__ __device__ static constexpr int row(int h, int x) { return GC == 1 ? 4 * h + x : 2 * h + x; }
+};
+
+template <int KB, int VB, bool QJL, int GC>
+struct Smem {
+    uint2 ktab[1 << (2 * KB)];          // (Ck hi|lo of c0, Ck hi|lo of c1) per pair of key codes
+    uint32_t vtab[1 << VB];             // Cv hi|lo per value code
+    uint32_t wt[NW][16][WT_STRIDE];     // per-wave transpose of the softmax weights
     union {
         struct {
-            float q[NH][D];
-            float qrot[NH][D];
-            float qproj[NH][D];
+            float q[8][D];
+            float qr[8][D];             // q R_k^T
+            float qp[8][D];             // q S^T, then its fixed-point integer image
+            float red[NT / 64];
         } pro;
-        float w[NWAVE][TILE][NH];  // p * |v| of the current tile, per wave
         struct {
-            float o[NWAVE][NH][D];
-            float m[NWAVE][NH];
-            float s[NWAVE][NH];
+            float o[NW][8][D];
+            float m[NW][8];
+            float s[NW][8];
         } epi;
     } u;
 };
 
-template <int KB, int VB, bool QJL, int G>
-__global__ __launch_bounds__(NT, MIN_WAVES_PER_SIMD) void split_kernel(
-    const uint16_t* __restrict__ q, int q_heads, int kv_heads, const int32_t* __restrict__ seq_starts,
+template <int KB, int VB, bool QJL, int GC>
+__global__ __launch_bounds__(NT) void split_kernel(
+    const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
     const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vn, const float* __restrict__ Rk,
     const float* __restrict__ Ck, const float* __restrict__ S, const float* __restrict__ Cv, float scale,
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
-    using Smem = SplitSmem<KB, VB, QJL, G>;
-    constexpr int NQ = Smem::NQ;
-    constexpr int NH = Smem::NH;
+    using Sm = Smem<KB, VB, QJL, GC>;
+    using R = Rows<GC>;
     constexpr int KROW = D * KB / 8;  // bytes per key row
     constexpr int VROW = D * VB / 8;  // bytes per value row
-    constexpr int KPAIR = 1 << (2 * KB);
-    constexpr int VPAIR = 1 << (2 * VB);
-    __shared__ Smem sm;
+    constexpr int VCH = 8 * VB;       // bits of one lane's 8-dim value chunk
+    __shared__ Sm sm;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, grp = blockIdx.y;
     const int b = grp / kv_heads, kvh = grp - b * kv_heads;
     const int bh0 = b * q_heads + kvh * G;  // first query head of the group
 
     // ------------------------------------------------------------ prologue
-    for (int i = tid; i < NH * D; i += NT) {
+    for (int i = tid; i < (1 << (2 * KB)); i += NT)
+        sm.ktab[i] = make_uint2(pack_hilo(Ck[i & ((1 << KB) - 1)]), pack_hilo(Ck[i >> KB]));
+    for (int i = tid; i < (1 << VB); i += NT) sm.vtab[i] = pack_hilo(Cv[i]);
+    for (int i = tid; i < 8 * D; i += NT) {
         const int h = i / D, d = i % D;
         sm.u.pro.q[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
     }
-    for (int i = tid; i < KPAIR; i += NT)
-        sm.lutk[i] = make_float2(Ck[i & ((1 << KB) - 1)], Ck[i >> KB]);
-    for (int i = tid; i < VPAIR; i += NT)
-        sm.lutv[i] = make_float2(Cv[i & ((1 << VB) - 1)], Cv[i >> VB]);
+    // rows of the weight transpose that never carry a head (GC = 1: rows 4h + 2, 4h + 3)
+    for (int i = tid; i < NW * 16 * WT_STRIDE; i += NT) (&sm.wt[0][0][0])[i] = 0u;
     __syncthreads();
-    {
-        // thread -> output row j, heads h = hp, hp + HS, ...: q_rot[h][j] = q[h] . Rk[j], q_proj[h][j] = q[h] . S[j]
-        constexpr int HS = NT / D;        // head slices (4 with 512 threads)
-        constexpr int HPER = (NH + HS - 1) / HS;
-        const int j = tid & (D - 1), hp = tid / D;
-        float ar[HPER], ap[HPER];
+    if (tid < 2 * D) {
+        // thread -> (matrix, output dim j): q_rot[h][j] = q[h] . R_k[j], q_proj[h][j] = q[h] . S[j]
+        const int j = tid & (D - 1);
+        const bool proj = tid >= D;
+        if (!proj || QJL) {
+            const float4* row = reinterpret_cast<const float4*>((proj ? S : Rk) + (size_t)j * D);
+            float acc[8];
 #pragma unroll
-        for (int i = 0; i < HPER; ++i) ar[i] = ap[i] = 0.0f;
-        const float4* rr = reinterpret_cast<const float4*>(Rk + (size_t)j * D);
-        const float4* sr = reinterpret_cast<const float4*>(S + (size_t)j * D);
-        for (int d4 = 0; d4 < D / 4; ++d4) {
-            const float4 r4 = rr[d4];
-            float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (QJL) s4 = sr[d4];
+            for (int h = 0; h < 8; ++h) acc[h] = 0.0f;
+            for (int d4 = 0; d4 < D / 4; ++d4) {
+                const float4 r4 = row[d4];
 #pragma unroll
-            for (int i = 0; i < HPER; ++i) {
-                if (hp + HS * i >= NH) break;
-                const float* qh = sm.u.pro.q[hp + HS * i] + 4 * d4;
-                ar[i] = __builtin_fmaf(qh[0], r4.x, ar[i]);
-                ar[i] = __builtin_fmaf(qh[1], r4.y, ar[i]);
-                ar[i] = __builtin_fmaf(qh[2], r4.z, ar[i]);
-                ar[i] = __builtin_fmaf(qh[3], r4.w, ar[i]);
-                if constexpr (QJL) {
-                    ap[i] = __builtin_fmaf(qh[0], s4.x, ap[i]);
-                    ap[i] = __builtin_fmaf(qh[1], s4.y, ap[i]);
-                    ap[i] = __builtin_fmaf(qh[2], s4.z, ap[i]);
-                    ap[i] = __builtin_fmaf(qh[3], s4.w, ap[i]);
+                for (int h = 0; h < 4 * GC; ++h) {
+                    const float* qh = sm.u.pro.q[h] + 4 * d4;
+                    acc[h] = __builtin_fmaf(qh[0], r4.x, acc[h]);
+                    acc[h] = __builtin_fmaf(qh[1], r4.y, acc[h]);
+                    acc[h] = __builtin_fmaf(qh[2], r4.z, acc[h]);
+                    acc[h] = __builtin_fmaf(qh[3], r4.w, acc[h]);
                 }
             }
-        }
 #pragma unroll
-        for (int i = 0; i < HPER; ++i) {
-            if (hp + HS * i >= NH) break;
-            sm.u.pro.qrot[hp + HS * i][j] = ar[i];
-            sm.u.pro.qproj[hp + HS * i][j] = ap[i];
+            for (int h = 0; h < 8; ++h) (proj ? sm.u.pro.qp : sm.u.pro.qr)[h][j] = acc[h];
         }
     }
     __syncthreads();
+
+    // fixed-point scale of q_proj: |q_proj * 2^F| <= 2^30, so four balanced int8 limbs hold it
+    int F = 0;
     if constexpr (QJL) {
-        // byte table of sum_i q_proj[8 pos + i] * (bit_i ? +1 : -1), by doubling:
-        // T[0] = -sum_i q_proj[8 pos + i];  T[b] = T[b - 2^k] + 2 q_proj[8 pos + k] for 2^k <= b < 2^(k+1)
-        for (int i = tid; i < NQ * 16; i += NT) {
-            const int qq = i / 16, pos = i % 16;
-            f4 t0 = {0.f, 0.f, 0.f, 0.f};
+        float mx = 0.0f;
+        for (int i = tid; i < 8 * D; i += NT) mx = fmaxf(mx, fabsf((&sm.u.pro.qp[0][0])[i]));
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) t0[r] -= sm.u.pro.qproj[4 * qq + r][8 * pos + k];
-            sm.lutq[i * 256] = t0;
-        }
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if (lane == 0) sm.u.pro.red[wave] = mx;
         __syncthreads();
-#pragma unroll 1
-        for (int k = 0; k < 8; ++k) {
-            const int span = 1 << k;
-            for (int i = tid; i < NQ * 16 * span; i += NT) {
-                const int qq = i / (16 * span), rem = i % (16 * span);
-                const int pos = rem / span, bb = span + rem % span;
-                const int d = 8 * pos + k;
-                const f4 add = {2.0f * sm.u.pro.qproj[4 * qq + 0][d], 2.0f * sm.u.pro.qproj[4 * qq + 1][d],
-                                2.0f * sm.u.pro.qproj[4 * qq + 2][d], 2.0f * sm.u.pro.qproj[4 * qq + 3][d]};
-                sm.lutq[(qq * 16 + pos) * 256 + bb] = sm.lutq[(qq * 16 + pos) * 256 + bb - span] + add;
+        mx = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm.u.pro.red[w]);
+        int e = 0;
+        if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
+        F = 30 - e;
+        F = F > 100 ? 100 : F;
+    }
+
+    // A operands of the key-score MFMAs (32 VGPRs): lane (i = n, g), MFMA j, VGPR r holds
+    // q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo codebook parts).
+    const int h_row = GC == 1 ? n / 4 : n / 2;
+    const int x_row = GC == 1 ? n % 4 : n % 2;
+    const bool row_live = x_row < 2 && h_row < G;
+    u32x4 qa[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint32_t v = 0;
+            if (row_live) {
+                uint32_t hi, lo;
+                split_bf16(sm.u.pro.qr[h_row][32 * g + 4 * j + r], hi, lo);
+                v = x_row == 0 ? hi : lo;
+                v |= v << 16;
             }
-            __syncthreads();
+            qa[j][r] = v;
+        }
+    // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj (dims of shift 4 jj + v),
+    // VGPR v, byte e <-> dim 32 g + 4 jj + v + 8 e.
+    u32x4 qj[R::NQJ][2];
+    float sq[R::HPL];  // sum_d q_proj_int[h][d] / 2^F for this lane's heads
+#pragma unroll
+    for (int i = 0; i < R::HPL; ++i) sq[i] = 0.0f;
+    if constexpr (QJL) {
+        const float sc = ldexpf(1.0f, F);
+#pragma unroll
+        for (int set = 0; set < R::NQJ; ++set) {
+            const int h = GC == 1 ? n / 4 : n / 2;
+            const int limb = GC == 1 ? n % 4 : 2 * set + (n % 2);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        int x = 0;
+                        if (h < G) x = (int)rintf(sm.u.pro.qp[h][32 * g + 4 * jj + v + 8 * e] * sc);
+                        // balanced base-256 digits: x = l0 + 256 l1 + 65536 l2 + 2^24 l3, l_i in [-128, 127]
+                        int digit = 0;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const int l = ((x + 128) & 255) - 128;
+                            if (k == limb) digit = l;
+                            x = (x - l) >> 8;
+                        }
+                        word |= (uint32_t)(digit & 255) << (8 * e);
+                    }
+                    qj[set][jj][v] = word;
+                }
+        }
+        // per-head sums of the integer images (for the +-1 form of the signs)
+#pragma unroll
+        for (int i = 0; i < R::HPL; ++i) {
+            const int h = R::HPL * g + i;
+            double acc = 0.0;
+            if (h < G)
+                for (int d = 0; d < D; ++d) acc += (double)rintf(sm.u.pro.qp[h][d] * sc);
+            sq[i] = (float)(acc * (double)ldexpf(1.0f, -F));
         }
     }
-    // A operands of the key MFMAs: lane (ts, g, j) holds q_rot[4 qq + j][32 g + k], k < 32
-    const int kg = (lane >> 2) & 3;  // 32-dim group of this lane in the key pass
-    const int kj = lane & 3;         // token within the 4-token MFMA block / head row
-    float qa[NQ][32];
-#pragma unroll
-    for (int qq = 0; qq < NQ; ++qq)
-#pragma unroll
-        for (int k = 0; k < 32; ++k) qa[qq][k] = sm.u.pro.qrot[4 * qq + kj][32 * kg + k];
-    __syncthreads();  // the prologue area is reused for the softmax weights
+    __syncthreads();  // the prologue area is reused by the epilogue
 
     // ---------------------------------------------------------- token range
     int64_t len = n_tokens;
@@ -240,246 +303,240 @@ __global__ __launch_bounds__(NT, MIN_WAVES_PER_SIMD) void split_kernel(
         const int64_t l = seq_lens[b];
         len = l < n_tokens ? (l < 0 ? 0 : l) : n_tokens;
     }
-    int64_t t0 = (int64_t)split * tokens_per_split;
-    const int64_t t1 = (t0 + tokens_per_split < len) ? t0 + tokens_per_split : len;
+    int64_t start = 0;
     if (seq_starts) {
         const int64_t st = seq_starts[b];
-        if (st > t0) t0 = st;
+        start = st < 0 ? 0 : st;
     }
+    int64_t r0 = (int64_t)split * tokens_per_split;
+    int64_t r1 = r0 + tokens_per_split;
+    r0 = r0 > start ? r0 : start;
+    r1 = r1 < len ? r1 : len;
+    const int64_t span = r1 > r0 ? r1 - r0 : 0;
+    const int64_t per_wave = ((span + NW - 1) / NW + BLK - 1) / BLK * BLK;
+    const int64_t t0 = r0 + (int64_t)wave * per_wave;
+    int64_t t1 = t0 + per_wave;
+    t1 = t1 < r1 ? t1 : r1;
     const size_t row0 = (size_t)grp * cap;
 
-    f4 m_run[NQ], dv[NQ][8];
-    float s_lane[NQ];
+    // per-lane softmax state (heads of this lane group) and value accumulators
+    float m_run[R::HPL], s_lane[R::HPL];
 #pragma unroll
-    for (int qq = 0; qq < NQ; ++qq) {
-        m_run[qq] = f4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
-        s_lane[qq] = 0.0f;
+    for (int i = 0; i < R::HPL; ++i) m_run[i] = NEG_INF, s_lane[i] = 0.0f;
+    f32x4 acc_v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) dv[qq][k] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-    const int kts = lane >> 4;         // 4-token set of this lane in the key pass
-    const int vs = lane >> 4;          // token slot of this lane in the value pass
-    const int vcnk = lane & 15;        // 8-dim chunk of this lane in the value pass
-    const int vboff = vcnk * VB;       // byte offset of the chunk's codes in a value row
-    float (*wbuf)[NH] = sm.u.w[wave];
+    for (int m = 0; m < 8; ++m) acc_v[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Loads are software-pipelined: the key data of tile i+1 is issued before the
-    // value pass of tile i, the value data of tile i before its key pass, so every
-    // load has half a tile of MFMA/VALU work to arrive.  Addresses are a uniform
-    // (SGPR) tile base plus a 32-bit lane offset; only the last, partial tile of a
-    // range clamps token indices and masks logits.
-    constexpr int VW = (VB == 3) ? 2 : 1;  // dwords per lane per value row (3-bit codes straddle)
-    const int64_t step = (int64_t)NWAVE * TILE;
-    const int kofs_lane = (4 * kts + kj) * KROW + kg * 4 * KB;   // bytes, within a 16-token sub-tile
-    const int sofs_lane = (4 * kts + kj) * (D / 8) + 4 * kg;
-    const int nofs_lane = 4 * kts + kj;                          // token, within a sub-tile
-    const int vofs_lane = vs * VROW + (vboff & ~3);              // bytes, within a 4-token set
-    const bool v_hi = (VW == 2) && ((vboff & 3) + VB > 4);
-    uint32_t kw[4][KB], ksw[4], kn16[4], kr16[4], vn16[4];
-    uint32_t vw[16][VW];
-    auto load_keys = [&](int64_t tb, bool masked) {
-        const uint8_t* kb = kc + (row0 + tb) * KROW;
-        const uint8_t* sb = ks + (row0 + tb) * (D / 8);
-        const uint16_t* nb = kn + row0 + tb;
-        const uint16_t* rb = kr + row0 + tb;
-        const uint16_t* vb = vn + row0 + tb;
-        const int last = (int)(t1 - 1 - tb);
+    const float c_mse = scale * LOG2E;
+    const float c_qjl = scale * LOG2E * QJL_SCALE;
+    const float qfix = ldexpf(1.0f, 1 - F);  // 2 * 2^-F: sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp
+    uint32_t(*wt)[WT_STRIDE] = sm.wt[wave];
+
+    // value chunk of lane n: dims [8n, 8n + 8) = bits [VCH n, VCH n + VCH) of the row
+    constexpr int VCH_BYTES_MAX = VROW;
+    const int vbit0 = VCH * n;
+    const int vdw = vbit0 >> 5;                       // first dword of the chunk
+    const int vsh = vbit0 & 31;
+    const bool v2 = (vsh + VCH > 32);                 // chunk straddles two dwords (VB = 3 only)
+    (void)VCH_BYTES_MAX;
+
+    struct Blk {
+        uint32_t kw[KB];     // key codes of token n, dims [32 g, 32 g + 32)
+        uint32_t sw;         // sign bits of token n, dims [32 g, 32 g + 32)
+        uint32_t kn, kr, vn; // norms (f16 bits) of token n
+        uint32_t vw[4][2];   // value codes of tokens 4 g + r, lane n's dword(s)
+    };
+    auto load = [&](Blk& B, int64_t tb) {
+        const int64_t last = t1 - 1;
+        int64_t tk = tb + n;
+        tk = tk < last ? tk : last;
+        const uint32_t* kp = reinterpret_cast<const uint32_t*>(kc + (row0 + tk) * KROW) + KB * g;
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            int tok = 16 * st + nofs_lane;
-            if (masked) tok = tok < last ? tok : last;
-            const int d = tok - nofs_lane - 16 * st;  // 0 unless clamped
-            const uint32_t* k32 = reinterpret_cast<const uint32_t*>(kb + 16 * st * KROW + kofs_lane + d * KROW);
+        for (int i = 0; i < KB; ++i) B.kw[i] = kp[i];
+        if constexpr (QJL) {
+            B.sw = reinterpret_cast<const uint32_t*>(ks + (row0 + tk) * (D / 8))[g];
+            B.kr = kr[row0 + tk];
+        } else {
+            B.sw = 0u;
+            B.kr = 0u;
+        }
+        B.kn = kn[row0 + tk];
+        B.vn = vn[row0 + tk];
 #pragma unroll
-            for (int i = 0; i < KB; ++i) kw[st][i] = k32[i];
-            kn16[st] = nb[tok];
-            vn16[st] = vb[tok];
+        for (int r = 0; r < 4; ++r) {
+            int64_t tv = tb + 4 * g + r;
+            tv = tv < last ? tv : last;
+            const uint32_t* vp = reinterpret_cast<const uint32_t*>(vc + (row0 + tv) * VROW) + vdw;
+            B.vw[r][0] = vp[0];
+            B.vw[r][1] = v2 ? vp[1] : 0u;  // never past the row: only straddling chunks read on
+        }
+    };
+
+    auto process = [&](const Blk& B, int64_t tb) {
+        // ---- key scores: 8 MFMAs over dims 32 g + 4 j + r
+        f32x4 acc_k = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            u32x4 bk;
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t off = field_x<2 * KB, 3>(B.kw, (4 * j + 2 * p) * KB);
+                const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.ktab) + off);
+                bk[2 * p] = e.x;
+                bk[2 * p + 1] = e.y;
+            }
+            acc_k = mfma_bf16(qa[j], bk, acc_k);
+        }
+        // ---- QJL sums
+        i32x4 acc_q[R::NQJ];
+        if constexpr (QJL) {
+#pragma unroll
+            for (int set = 0; set < R::NQJ; ++set) {
+                acc_q[set] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    u32x4 bq;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) bq[v] = (B.sw >> (4 * jj + v)) & 0x01010101u;
+                    acc_q[set] = mfma_i8(qj[set][jj], bq, acc_q[set]);
+                }
+            }
+        }
+        // ---- scores (log2 domain) of token n for this lane's heads
+        const bool valid = tb + n < t1;
+        const float knf = tq::f16_to_f32(B.kn) * c_mse;
+        const float krf = QJL ? tq::f16_to_f32(B.kr) * c_qjl : 0.0f;
+        const float vnf = tq::f16_to_f32(B.vn);
+        float lg[R::HPL];
+#pragma unroll
+        for (int i = 0; i < R::HPL; ++i) {
+            float v = knf * (acc_k[2 * i] + acc_k[2 * i + 1]);
             if constexpr (QJL) {
-                ksw[st] = *reinterpret_cast<const uint32_t*>(sb + 16 * st * (D / 8) + sofs_lane + d * (D / 8));
-                kr16[st] = rb[tok];
+                float qs;
+                if constexpr (GC == 1) {
+                    qs = ((float)acc_q[0][0] + 256.0f * (float)acc_q[0][1]) +
+                         (65536.0f * (float)acc_q[0][2] + 16777216.0f * (float)acc_q[0][3]);
+                } else {
+                    qs = ((float)acc_q[0][2 * i] + 256.0f * (float)acc_q[0][2 * i + 1]) +
+                         (65536.0f * (float)acc_q[1][2 * i] + 16777216.0f * (float)acc_q[1][2 * i + 1]);
+                }
+                v = __builtin_fmaf(krf, __builtin_fmaf(qs, qfix, -sq[i]), v);
+            }
+            lg[i] = valid ? v : NEG_INF;
+        }
+        // ---- online softmax
+        bool grow = false;
+        float mnew[R::HPL];
+#pragma unroll
+        for (int i = 0; i < R::HPL; ++i) {
+            mnew[i] = fmaxf(m_run[i], row_max16(lg[i]));
+            grow |= mnew[i] > m_run[i];
+        }
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+            for (int i = 0; i < R::HPL; ++i) {
+                const float a = m_run[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_run[i] - mnew[i]);
+                s_lane[i] *= a;
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {
+                    acc_v[m][2 * i] *= a;
+                    acc_v[m][2 * i + 1] *= a;
+                }
+                m_run[i] = mnew[i];
             }
         }
-    };
-    auto load_values = [&](int64_t tb, bool masked) {
-        const uint8_t* base = vc + (row0 + tb) * VROW;
-        const int last = (int)(t1 - 1 - tb);
+        uint32_t wq[R::HPL][2];
 #pragma unroll
-        for (int it = 0; it < 16; ++it) {
-            int ofs = 4 * it * VROW + vofs_lane;
-            if (masked && 4 * it + vs > last) ofs = last * VROW + (vboff & ~3);
-            const uint32_t* v32 = reinterpret_cast<const uint32_t*>(base + ofs);
-            vw[it][0] = v32[0];
-            // second dword only where the lane's 3-byte chunk straddles it (never past the row)
-            if constexpr (VW == 2) vw[it][1] = v_hi ? v32[1] : 0u;
+        for (int i = 0; i < R::HPL; ++i) {
+            const float mu = m_run[i] == NEG_INF ? 0.0f : m_run[i];
+            const float p = __builtin_amdgcn_exp2f(lg[i] - mu);
+            s_lane[i] += p;
+            uint32_t hi, lo;
+            split_bf16(p * vnf, hi, lo);
+            wq[i][0] = hi | (hi << 16);
+            wq[i][1] = lo | (lo << 16);
         }
-    };
-    auto tile = [&](int64_t tb, bool masked) {
-        // ------------------------------------------------------ key pass
-        f4 lg[4][NQ];
-        float vnorm[4];
+        // ---- weights -> A operand of the value MFMAs (transpose through LDS)
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const bool valid = !masked || tb + 16 * st + nofs_lane < t1;
-            const float knf = tq::f16_to_f32(kn16[st]) * scale;
-            vnorm[st] = tq::f16_to_f32(vn16[st]);
-            f4 acc0[NQ], acc1[NQ];
-#pragma unroll
-            for (int qq = 0; qq < NQ; ++qq) acc0[qq] = acc1[qq] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int p = 0; p < 16; ++p) {
-                const float2 c = sm.lutk[tq::extract_bits<2 * KB>(kw[st], 2 * KB * p)];
-#pragma unroll
-                for (int qq = 0; qq < NQ; ++qq) {
-                    acc0[qq] = mfma4x4(qa[qq][2 * p], c.x, acc0[qq]);
-                    acc1[qq] = mfma4x4(qa[qq][2 * p + 1], c.y, acc1[qq]);
-                }
-            }
-            float qsc = 0.0f;
-            if constexpr (QJL) qsc = (QJL_SCALE * scale) * tq::f16_to_f32(kr16[st]);
-#pragma unroll
-            for (int qq = 0; qq < NQ; ++qq) {
-                f4 part = (acc0[qq] + acc1[qq]) * knf;
-                if constexpr (QJL) {
-                    const uint32_t sw = ksw[st];
-                    const f4* tab = sm.lutq + (qq * 16 + 4 * kg) * 256;
-                    const f4 qj = (tab[__builtin_amdgcn_ubfe(sw, 0, 8)] + tab[256 + __builtin_amdgcn_ubfe(sw, 8, 8)]) +
-                                  (tab[512 + __builtin_amdgcn_ubfe(sw, 16, 8)] + tab[768 + (sw >> 24)]);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) part[r] = __builtin_fmaf(qsc, qj[r], part[r]);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float v = part[r];
-                    v += dpp<DPP_ROR4>(v);
-                    v += dpp<DPP_ROR8>(v);
-                    lg[st][qq][r] = valid ? v : NEG_INF;
-                }
-            }
+        for (int i = 0; i < R::HPL; ++i) {
+            const int h = R::HPL * g + i;
+            wt[R::row(h, 0)][n] = wq[i][0];
+            wt[R::row(h, 1)][n] = wq[i][1];
         }
-        if (tb + step < t1) load_keys(tb + step, tb + step + TILE > t1);
-        // ------------------------------------------------------ online softmax
-        f4 alpha[NQ];
-        bool rescale = false;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
+        // ---- value MFMAs: lane (n, g) supplies tokens 4 g + r, dim 8 n + m
+        uint32_t vch[4];
 #pragma unroll
-        for (int qq = 0; qq < NQ; ++qq) {
+        for (int r = 0; r < 4; ++r) {
+            if constexpr (VB == 3)
+                vch[r] = __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh);
+            else
+                vch[r] = B.vw[r][0] >> vsh;
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            u32x4 bv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float mt = fmaxf(fmaxf(lg[0][qq][r], lg[1][qq][r]), fmaxf(lg[2][qq][r], lg[3][qq][r]));
-                mt = max_tokens(mt);
-                const float mn = fmaxf(m_run[qq][r], mt);  // finite: the tile has a valid token
-                rescale |= m_run[qq][r] != mn;
-                alpha[qq][r] = __expf(m_run[qq][r] - mn);
-                m_run[qq][r] = mn;
+                const uint32_t off = field_x<VB, 2>(&vch[r], VB * m);
+                bv[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.vtab) + off);
             }
-            // this lane's head in the weight table is 4 qq + kg
-            const float mh = sel4(m_run[qq], kg);
-            float ps = 0.0f;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const float p = __expf(sel4(lg[st][qq], kg) - mh);  // exp(-inf) = 0 for invalid tokens
-                ps += p;
-                wbuf[16 * st + nofs_lane][4 * qq + kg] = (4 * qq + kg < G) ? p * vnorm[st] : 0.0f;
-            }
-            s_lane[qq] = rescale ? __builtin_fmaf(s_lane[qq], sel4(alpha[qq], kg), ps) : s_lane[qq] + ps;
+            acc_v[m] = mfma_bf16(av, bv, acc_v[m]);
         }
-        if (rescale) {
-#pragma unroll
-            for (int qq = 0; qq < NQ; ++qq)
-#pragma unroll
-                for (int k = 0; k < 8; ++k) dv[qq][k] *= alpha[qq];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        // ------------------------------------------------------ value pass
-#pragma unroll
-        for (int it = 0; it < 16; ++it) {
-            const int tt = 4 * it + vs;
-            uint32_t bits;
-            if constexpr (VW == 2) {
-                bits = __builtin_amdgcn_alignbit(vw[it][1], vw[it][0], 8 * (vboff & 3));
-            } else {
-                bits = vw[it][0] >> (8 * (vboff & 3));
-            }
-            float w[NQ];
-#pragma unroll
-            for (int qq = 0; qq < NQ; ++qq) w[qq] = wbuf[tt][4 * qq + kj];
-#pragma unroll
-            for (int k2 = 0; k2 < 4; ++k2) {
-                const float2 c = sm.lutv[__builtin_amdgcn_ubfe(bits, 2 * VB * k2, 2 * VB)];
-#pragma unroll
-                for (int qq = 0; qq < NQ; ++qq) {
-                    dv[qq][2 * k2] = mfma4x4(w[qq], c.x, dv[qq][2 * k2]);
-                    dv[qq][2 * k2 + 1] = mfma4x4(w[qq], c.y, dv[qq][2 * k2 + 1]);
-                }
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
-    int64_t tb = t0 + (int64_t)wave * TILE;
-    if (tb < t1) load_keys(tb, tb + TILE > t1);
-    for (; tb + TILE <= t1; tb += step) {  // full tiles
-        load_values(tb, false);
-        tile(tb, false);
-    }
-    if (tb < t1) {  // the partial tile (at most one per wave)
-        load_values(tb, true);
-        tile(tb, true);
+
+    if (t0 < t1) {
+        // two blocks in flight: while one is processed the next-but-one is loaded into
+        // the register set just consumed, so the roles of A and Bq alternate without copies
+        Blk A, Bq;
+        int64_t tb = t0;
+        load(A, tb);
+        if (tb + BLK < t1) load(Bq, tb + BLK);
+        while (true) {
+            process(A, tb);
+            tb += BLK;
+            if (tb >= t1) break;
+            if (tb + BLK < t1) load(A, tb + BLK);
+            process(Bq, tb);
+            tb += BLK;
+            if (tb >= t1) break;
+            if (tb + BLK < t1) load(Bq, tb + BLK);
+        }
     }
 
     // ------------------------------------------------------------ epilogue
-    // value accumulators: lanes vcnk, +16, +32, +48 hold the same dims (token slots)
+    float s_row[R::HPL];
 #pragma unroll
-    for (int qq = 0; qq < NQ; ++qq)
+    for (int i = 0; i < R::HPL; ++i) s_row[i] = row_sum16(s_lane[i]);
+    // lane (n, g): dims 8 n + m of heads R::HPL g + i
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+    for (int i = 0; i < R::HPL; ++i) {
+        const int h = R::HPL * g + i;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = dv[qq][k][r];
-                v += swz_xor16(v);
-                v += __shfl_xor(v, 32);
-                dv[qq][k][r] = v;
-            }
-    // running sums: lane holds head 4 qq + kg over its tokens; sum over (kts, kj)
-#pragma unroll
-    for (int qq = 0; qq < NQ; ++qq) {
-        float v = s_lane[qq];
-        v += dpp<DPP_QUAD_XOR1>(v);
-        v += dpp<DPP_QUAD_XOR2>(v);
-        v += swz_xor16(v);
-        v += __shfl_xor(v, 32);
-        s_lane[qq] = v;
-    }
-    __syncthreads();  // weight buffers are reused for the wave merge
-    if (lane < 16) {
-#pragma unroll
-        for (int qq = 0; qq < NQ; ++qq)
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sm.u.epi.o[wave][4 * qq + r][8 * vcnk + k] = dv[qq][k][r];
-    }
-    if (lane < 4) {  // lanes 0..3 have kg = 0, kj = lane
-#pragma unroll
-        for (int qq = 0; qq < NQ; ++qq) sm.u.epi.m[wave][4 * qq + lane] = sel4(m_run[qq], lane);
-    }
-    if ((lane & 3) == 0 && lane < 16) {  // lanes 0, 4, 8, 12 hold kg = 0..3
-#pragma unroll
-        for (int qq = 0; qq < NQ; ++qq) sm.u.epi.s[wave][4 * qq + kg] = s_lane[qq];
+        for (int m = 0; m < 8; ++m) sm.u.epi.o[wave][h][8 * n + m] = acc_v[m][2 * i] + acc_v[m][2 * i + 1];
+        if (n == 0) {
+            sm.u.epi.m[wave][h] = m_run[i];
+            sm.u.epi.s[wave][h] = s_row[i];
+        }
     }
     __syncthreads();
     for (int i = tid; i < G * D; i += NT) {
         const int h = i / D, d = i % D;
         float M = NEG_INF;
 #pragma unroll
-        for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, sm.u.epi.m[w][h]);
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.u.epi.m[w][h]);
         float o = 0.0f, s = 0.0f;
         if (M != NEG_INF) {
 #pragma unroll
-            for (int w = 0; w < NWAVE; ++w) {
-                const float e = __expf(sm.u.epi.m[w][h] - M);
+            for (int w = 0; w < NW; ++w) {
+                const float mw = sm.u.epi.m[w][h];
+                const float e = mw == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
                 o = __builtin_fmaf(e, sm.u.epi.o[w][h][d], o);
                 s = __builtin_fmaf(e, sm.u.epi.s[w][h], s);
             }
@@ -494,37 +551,35 @@ __global__ __launch_bounds__(NT, MIN_WAVES_PER_SIMD) void split_kernel(
 }
 
 // ----------------------------------------------------------------- merge
+// One workgroup per (batch row, query head): merge the split partials (maxima in
+// the log2 domain), normalise, un-rotate by R_v.
 __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                                                   int n_split, const float* __restrict__ Rv,
                                                   float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
                                                   float* __restrict__ lse_out) {
     __shared__ float so[D];
-    __shared__ float se[D];  // per-split weights (n_split <= D is enforced on the host)
-    __shared__ float sM, sS;
-    const int bh = blockIdx.x, d = threadIdx.x;
+    __shared__ float red[2];
+    const int bh = blockIdx.x, d = threadIdx.x, lane = d & 63, wv = d >> 6;
     const float* ml = part_ml + (size_t)bh * n_split * 2;
-    float mv = d < n_split ? ml[2 * d] : NEG_INF;
-    float M = mv;
+    float M = NEG_INF;
+    for (int k = d; k < n_split; k += D) M = fmaxf(M, ml[2 * k]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (d == 0 || d == 64) se[d] = M;
+    if (lane == 0) red[wv] = M;
     __syncthreads();
-    M = fmaxf(se[0], se[64]);
+    M = fmaxf(red[0], red[1]);
     __syncthreads();
-    float e = (d < n_split && M != NEG_INF) ? __expf(mv - M) : 0.0f;
-    float s = d < n_split ? e * ml[2 * d + 1] : 0.0f;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    se[d] = e;
-    if (d == 0) sS = s;
-    __syncthreads();
-    if (d == 64) sS += s;
-    __syncthreads();
-    const float sum = sS;
-    float o = 0.0f;
-    for (int k = 0; k < n_split; ++k) o = __builtin_fmaf(se[k], part_o[((size_t)bh * n_split + k) * D + d], o);
-    o = (M != NEG_INF) ? o / fmaxf(sum, 1e-8f) : 0.0f;
-    if (lse_out && d == 0) lse_out[bh] = (M != NEG_INF) ? M + logf(sum) : NEG_INF;
+    float o = 0.0f, s = 0.0f;
+    if (M != NEG_INF) {
+        for (int k = 0; k < n_split; ++k) {
+            const float mk = ml[2 * k];
+            const float e = mk == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
+            o = __builtin_fmaf(e, part_o[((size_t)bh * n_split + k) * D + d], o);
+            s = __builtin_fmaf(e, ml[2 * k + 1], s);
+        }
+    }
+    o = (M != NEG_INF) ? o / fmaxf(s, 1e-8f) : 0.0f;
+    if (lse_out && d == 0) lse_out[bh] = (M != NEG_INF) ? M * LN2 + logf(s) : NEG_INF;
     so[d] = o;
     __syncthreads();
     float a = 0.0f;
@@ -536,7 +591,7 @@ __global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ part
 
 struct SplitArgs {
     const uint16_t* q;
-    int q_heads, kv_heads;
+    int q_heads, kv_heads, G;
     const int32_t *seq_starts, *seq_lens;
     int64_t n_tokens, cap;
     const uint8_t* kc;
@@ -552,27 +607,83 @@ struct SplitArgs {
     float *po, *pml;
 };
 
-template <int KB, int VB, bool QJL, int G>
-void launch_split(const SplitArgs& a, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, G>), grid, dim3(NT), 0, s, a.q, a.q_heads, a.kv_heads,
-                       a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc, a.vn, a.Rk, a.Ck,
-                       a.S, a.Cv, a.scale, a.tps, a.n_split, a.po, a.pml);
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 256;
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 256;
+        cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    }
+    return cus;
+}
+
+template <int KB, int VB, bool QJL, int GC>
+int wgs_per_cu() {
+    static int occ = 0;
+    if (occ == 0) {
+        int o = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, NT, 0) != hipSuccess || o < 1)
+            o = 1;
+        occ = o;
+    }
+    return occ;
+}
+
+int choose_split(int groups, int64_t n_tokens, int target_wgs, int64_t* tokens_per_split) {
+    const int64_t min_per_split = (int64_t)NW * BLK * 2;  // >= two blocks per wave
+    const int64_t max_split = (n_tokens + min_per_split - 1) / min_per_split;
+    int64_t want = (target_wgs + groups - 1) / groups;
+    const int64_t cap_split = (MAX_RESIDENT_WGS + groups - 1) / groups;
+    want = want < cap_split ? want : cap_split;
+    int64_t ns = want < max_split ? want : max_split;
+    if (ns < 1) ns = 1;
+    int64_t per = (n_tokens + ns - 1) / ns;
+    per = (per + BLK - 1) / BLK * BLK;
+    if (per < BLK) per = BLK;
+    *tokens_per_split = per;
+    const int64_t got = (n_tokens + per - 1) / per;
+    return (int)(got > 0 ? got : 1);
+}
+
+template <int KB, int VB, bool QJL, int GC>
+int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out, int64_t* tps_out) {
+    const int target = wgs_per_cu<KB, VB, QJL, GC>() * cu_count();
+    int64_t tps;
+    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, &tps);
+    *n_split_out = ns;
+    *tps_out = tps;
+    if (a.po == nullptr) return TQ_OK;  // sizing query only
+    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(NT), 0, s, a.q, a.q_heads,
+                       a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
+                       a.vn, a.Rk, a.Ck, a.S, a.Cv, a.scale, tps, ns, a.po, a.pml);
+    return TQ_OK;
 }
 
 template <int KB, int VB, bool QJL>
-int launch_split_g(int G, const SplitArgs& a, dim3 grid, hipStream_t s) {
-    switch (G) {
-        case 1: launch_split<KB, VB, QJL, 1>(a, grid, s); break;
-        case 2: launch_split<KB, VB, QJL, 2>(a, grid, s); break;
-        case 3: launch_split<KB, VB, QJL, 3>(a, grid, s); break;
-        case 4: launch_split<KB, VB, QJL, 4>(a, grid, s); break;
-        case 5: launch_split<KB, VB, QJL, 5>(a, grid, s); break;
-        case 6: launch_split<KB, VB, QJL, 6>(a, grid, s); break;
-        case 7: launch_split<KB, VB, QJL, 7>(a, grid, s); break;
-        case 8: launch_split<KB, VB, QJL, 8>(a, grid, s); break;
-        default: return TQ_ERR_UNSUPPORTED;
+int launch_split_g(int G, const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
+    if (G <= 4) return launch_split<KB, VB, QJL, 1>(a, groups, s, ns, tps);
+    if (G <= 8) return launch_split<KB, VB, QJL, 2>(a, groups, s, ns, tps);
+    return TQ_ERR_UNSUPPORTED;
+}
+
+int dispatch(int key_bits, int value_bits, int has_qjl, int G, const SplitArgs& a, int groups, hipStream_t s,
+             int* ns, int64_t* tps) {
+    if (has_qjl) {
+        switch (value_bits) {
+            case 2: return launch_split_g<1, 2, true>(G, a, groups, s, ns, tps);
+            case 3: return launch_split_g<2, 3, true>(G, a, groups, s, ns, tps);
+            default: return launch_split_g<3, 4, true>(G, a, groups, s, ns, tps);
+        }
     }
-    return TQ_OK;
+    switch (value_bits) {
+        case 1: return launch_split_g<1, 1, false>(G, a, groups, s, ns, tps);
+        case 2: return launch_split_g<2, 2, false>(G, a, groups, s, ns, tps);
+        case 3: return launch_split_g<3, 3, false>(G, a, groups, s, ns, tps);
+        default: return launch_split_g<4, 4, false>(G, a, groups, s, ns, tps);
+    }
+    (void)key_bits;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -582,9 +693,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 extern "C" size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, int kv_heads, int dim,
                                                       int64_t max_tokens) {
     if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || dim != D || max_tokens < 0) return 0;
-    // any n_tokens yields at most ceil(TARGET_WGS / groups) splits
+    // any n_tokens yields at most ceil(MAX_RESIDENT_WGS / groups) splits
     const int64_t groups = (int64_t)batch * kv_heads;
-    const int bound = (int)((TARGET_WGS + groups - 1) / groups);
+    const int bound = (int)((MAX_RESIDENT_WGS + groups - 1) / groups);
     return ws_layout(batch, q_heads, bound).total;
 }
 
@@ -615,38 +726,24 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     if (!workspace) return TQ_ERR_WORKSPACE;
     if (!(scale > 0.0f)) scale = 1.0f / sqrtf((float)D);
 
-    int64_t tps;
-    const int n_split = choose_split(batch * kv_heads, n_tokens > 0 ? n_tokens : 1, &tps);
-    if (n_split > D) return TQ_ERR_UNSUPPORTED;  // merge kernel keeps one weight per thread
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int groups = batch * kv_heads;
+    SplitArgs a{q, q_heads, kv_heads, G, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms,
+                v_codes, v_norms, key_rotation, key_centers, qjl, value_centers, scale, 0, 0, nullptr, nullptr};
+    int n_split = 0;
+    int64_t tps = 0;
+    int st = dispatch(key_bits, value_bits, has_qjl, G, a, groups, s, &n_split, &tps);  // sizing
+    if (st != TQ_OK) return st;
     const Ws w = ws_layout(batch, q_heads, n_split);
     if (workspace_bytes < w.total) return TQ_ERR_WORKSPACE;
     char* base = static_cast<char*>(workspace);
-    float* po = reinterpret_cast<float*>(base + w.po);
-    float* pml = reinterpret_cast<float*>(base + w.pml);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-
-    SplitArgs a{q, q_heads, kv_heads, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms,
-                v_codes, v_norms, key_rotation, key_centers, qjl, value_centers, scale, tps, n_split, po, pml};
-    const dim3 grid(n_split, batch * kv_heads);
-    int st;
-    if (has_qjl) {
-        switch (value_bits) {
-            case 2: st = launch_split_g<1, 2, true>(G, a, grid, s); break;
-            case 3: st = launch_split_g<2, 3, true>(G, a, grid, s); break;
-            default: st = launch_split_g<3, 4, true>(G, a, grid, s); break;
-        }
-    } else {
-        switch (value_bits) {
-            case 1: st = launch_split_g<1, 1, false>(G, a, grid, s); break;
-            case 2: st = launch_split_g<2, 2, false>(G, a, grid, s); break;
-            case 3: st = launch_split_g<3, 3, false>(G, a, grid, s); break;
-            default: st = launch_split_g<4, 4, false>(G, a, grid, s); break;
-        }
-    }
+    a.po = reinterpret_cast<float*>(base + w.po);
+    a.pml = reinterpret_cast<float*>(base + w.pml);
+    st = dispatch(key_bits, value_bits, has_qjl, G, a, groups, s, &n_split, &tps);
     if (st != TQ_OK) return st;
     TQ_CHECK_LAUNCH();
-    hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(D), 0, s, po, pml, n_split, value_rotation, out_f32,
-                       out_bf16, lse_out);
+    hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(D), 0, s, a.po, a.pml, n_split, value_rotation,
+                       out_f32, out_bf16, lse_out);
     TQ_CHECK_LAUNCH();
     return TQ_OK;
 }
