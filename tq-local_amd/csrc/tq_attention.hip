@@ -8,8 +8,9 @@
 //                 blocks of 16 tokens.  All G query heads of the GQA group share
 //                 every K/V byte read (reference runtime/triton_kernels.py:84-198
 //                 re-reads the tile once per query head).
-//   merge_kernel  log-sum-exp merge over splits, normalise, un-rotate by R_v, write
-//                 fp32 / bf16 / lse (reference :330-336, 366-368).
+//   merge_kernel  one workgroup per (batch row, KV head): log-sum-exp merge over
+//                 splits, normalise, un-rotate by R_v (read once for the G heads),
+//                 write fp32 / bf16 / lse (reference :330-336, 366-368).
 //
 // Per 16-token block, lane l = (n = l & 15, g = l >> 4):
 //
@@ -19,36 +20,57 @@
 //                 value); B = the dequantised keys, one 8-byte LDS lookup per pair of
 //                 codes returning (Ck_hi, Ck_lo) for both.  Every cross product of the
 //                 two-term splits is formed, so the score carries ~2^-17 relative error
-//                 against fp32 inputs (the fp32 reference rounds at 2^-24; the
-//                 tolerance is 2e-3 of |out|).
+//                 against fp32 inputs (the tolerance is 2e-3 of |out|).
 //   QJL term      v_mfma_i32_16x16x64_i8 on the raw sign bits (bytes of 0/1, two VALU
 //                 ops per 4 dims) against q_proj = q S^T in 32-bit fixed point split in
 //                 four int8 limbs (rows = (head, limb)); exact integer accumulation.
-//   softmax       online, base 2 (scores are pre-multiplied by log2 e), per head.
+//   softmax       online, base 2 (scores are pre-multiplied by log2 e), with a lazily
+//                 raised reference maximum: weights are exp2(score - m_ref) and m_ref
+//                 is raised (with a rescale of the partial sums) only when a score
+//                 exceeds it by more than 2^8, so blocks pay no cross-lane reduction.
 //   value sum     v_mfma_f32_16x16x32_bf16, D[(head, w hi|lo)][dim] += A B: A = the
 //                 softmax weights p |v| split hi/lo, transposed through LDS; B = value
 //                 codes dequantised by single-code LDS lookups (Cv_hi, Cv_lo) from a
 //                 table small enough to be bank-conflict free.
 //
-// Everything accumulates in fp32 (MFMA f32 / i32 accumulators); no packed-fp32 VALU.
+// All global reads are buffer loads against per-wave descriptors whose size is the
+// wave's token range: a lane offset fixed for the call plus a scalar block offset,
+// and reads past the range return zeros (no per-lane clamping or 64-bit address
+// arithmetic).  Everything accumulates in fp32 (MFMA f32 / i32); no packed-fp32 VALU.
 
 #include "tq_common.h"
 
 namespace {
 
 constexpr int D = TQ_DIM;
-constexpr int NW = 8;          // waves per split workgroup
-constexpr int NT = NW * 64;    // threads per split workgroup
+// waves per split workgroup: 3 per SIMD where the registers allow it (at most 4 query
+// heads per KV head), 2 per SIMD otherwise
+#ifndef TQ_ATTN_WAVES_G4
+#define TQ_ATTN_WAVES_G4 12
+#endif
+#ifndef TQ_ATTN_WAVES_G8
+#define TQ_ATTN_WAVES_G8 8
+#endif
+template <int GC>
+struct Cfg {
+    static constexpr int NW = GC == 1 ? TQ_ATTN_WAVES_G4 : TQ_ATTN_WAVES_G8;
+    static constexpr int NT = NW * 64;
+};
 constexpr int BLK = 16;        // tokens per block (MFMA N)
 constexpr int WT_STRIDE = 20;  // dwords per row of the weight-transpose buffer (bank spread)
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float QJL_SCALE = 1.2533141373155003f / D;  // sqrt(pi/2) / D
+constexpr float LAZY_MAX = 8.0f;                      // log2 headroom before the reference max is raised
+constexpr int BUF_DW3 = 0x00020000;                   // buffer descriptor word 3 (gfx9: 32-bit untyped)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4 c) {
@@ -60,15 +82,21 @@ __device__ __forceinline__ i32x4 mfma_i8(const u32x4& a, const u32x4& b, i32x4 c
                                                  0);
 }
 
-// bf16 (round to nearest even) of x and of the remainder x - bf16(x): x = hi + lo to ~2^-17.
-__device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo) {
-    hi = tq::f32_to_bf16(x);
-    lo = tq::f32_to_bf16(x - tq::bf16_to_f32(hi));
+// bf16 RNE (v_cvt_pk_bf16_f32) of x, and of the remainder x - bf16(x): x = hi + lo to ~2^-17.
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x);
 }
+__device__ __forceinline__ float bf16_val(uint32_t h) { return __uint_as_float(h << 16); }
+// (hi, lo) packed low | high
 __device__ __forceinline__ uint32_t pack_hilo(float x) {
-    uint32_t hi, lo;
-    split_bf16(x, hi, lo);
-    return hi | (lo << 16);
+    const __bf16 hi = (__bf16)x;
+    const __bf16 lo = (__bf16)(x - (float)hi);
+    return __builtin_bit_cast(uint32_t, bf16x2{hi, lo});
+}
+// (v, v) packed
+__device__ __forceinline__ uint32_t dup_bf16(float v) {
+    const __bf16 h = (__bf16)v;
+    return __builtin_bit_cast(uint32_t, bf16x2{h, h});
 }
 
 template <int CTRL>
@@ -106,6 +134,11 @@ __device__ __forceinline__ uint32_t field_x(const uint32_t* w, int pos) {
     return (w[wi] << (S - sh)) & M;
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+    const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, BUF_DW3);
+}
+
 struct Ws {
     size_t po, pml, total;
 };
@@ -122,8 +155,8 @@ Ws ws_layout(int batch, int q_heads, int n_split) {
 }
 
 // Upper bound on splits per group for any token count: the grid never exceeds
-// MAX_RESIDENT_WGS workgroups (more would queue behind the first wave of them).
-constexpr int MAX_RESIDENT_WGS = 256 * 4;
+// MAX_WGS workgroups.
+constexpr int MAX_WGS = 1024;
 
 // ------------------------------------------------------------------ split kernel
 // GC = 1: at most 4 query heads per KV head; row 4h + x of every MFMA belongs to
@@ -131,33 +164,38 @@ constexpr int MAX_RESIDENT_WGS = 256 * 4;
 // GC = 2: 5..8 heads; rows 2h + x, lane group g holds heads 2g and 2g + 1.
 template <int GC>
 struct Rows {
-    static constexpr int HPL = GC;      // heads per lane group
-    static constexpr int NQJ = GC;      // QJL MFMA sets (4 limbs per head in total)
+    static constexpr int HPL = GC;  // heads per lane group
+    static constexpr int NQJ = GC;  // QJL MFMA sets (four limbs per head in total)
+    static constexpr int NH = 4 * GC;
     __host__ __device__ static constexpr int row(int h, int x) { return GC == 1 ? 4 * h + x : 2 * h + x; }
 };
 
 template <int KB, int VB, bool QJL, int GC>
 struct Smem {
+    static constexpr int NH = 4 * GC;
+    static constexpr int NW = Cfg<GC>::NW;
     uint2 ktab[1 << (2 * KB)];          // (Ck hi|lo of c0, Ck hi|lo of c1) per pair of key codes
     uint32_t vtab[1 << VB];             // Cv hi|lo per value code
     uint32_t wt[NW][16][WT_STRIDE];     // per-wave transpose of the softmax weights
     union {
         struct {
-            float q[8][D];
-            float qr[8][D];             // q R_k^T
-            float qp[8][D];             // q S^T, then its fixed-point integer image
-            float red[NT / 64];
+            float q[NH][D];
+            float qr[NH][D];            // q R_k^T
+            float qp[NH][D];            // q S^T
+            uint32_t limb[4][NH][4][8]; // limb l of head h: [g][shift] -> 4 bytes (dims 32g + s + 8e)
+            float sq[NH];               // sum_d int(q_proj * 2^F) / 2^F
+            float red[NW];
         } pro;
         struct {
-            float o[NW][8][D];
-            float m[NW][8];
-            float s[NW][8];
+            float o[NW][NH][D];
+            float m[NW][NH];
+            float s[NW][NH];
         } epi;
     } u;
 };
 
 template <int KB, int VB, bool QJL, int GC>
-__global__ __launch_bounds__(NT) void split_kernel(
+__global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
@@ -166,22 +204,61 @@ __global__ __launch_bounds__(NT) void split_kernel(
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
     using Sm = Smem<KB, VB, QJL, GC>;
     using R = Rows<GC>;
+    constexpr int NW = Cfg<GC>::NW;
+    constexpr int NT = Cfg<GC>::NT;
+    constexpr int NH = R::NH;
     constexpr int KROW = D * KB / 8;  // bytes per key row
     constexpr int VROW = D * VB / 8;  // bytes per value row
     constexpr int VCH = 8 * VB;       // bits of one lane's 8-dim value chunk
     __shared__ Sm sm;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int n = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, grp = blockIdx.y;
     const int b = grp / kv_heads, kvh = grp - b * kv_heads;
     const int bh0 = b * q_heads + kvh * G;  // first query head of the group
 
+    // ---------------------------------------------------------- token range
+    // per-row bounds, made provably wave-uniform so the buffer descriptors below live in SGPRs
+    int64_t len = n_tokens;
+    if (seq_lens) {
+        const int64_t l = __builtin_amdgcn_readfirstlane(seq_lens[b]);
+        len = l < n_tokens ? (l < 0 ? 0 : l) : n_tokens;
+    }
+    int64_t start = 0;
+    if (seq_starts) {
+        const int64_t st = __builtin_amdgcn_readfirstlane(seq_starts[b]);
+        start = st < 0 ? 0 : st;
+    }
+    int64_t r0 = (int64_t)split * tokens_per_split;
+    int64_t r1 = r0 + tokens_per_split;
+    r0 = r0 > start ? r0 : start;
+    r1 = r1 < len ? r1 : len;
+    const int64_t span = r1 > r0 ? r1 - r0 : 0;
+    const int64_t per_wave = ((span + NW - 1) / NW + BLK - 1) / BLK * BLK;
+    const int64_t t0 = r0 + (int64_t)wave * per_wave;
+    int64_t t1 = t0 + per_wave;
+    t1 = t1 < r1 ? t1 : r1;
+    const int64_t ntok = t1 > t0 ? t1 - t0 : 0;
+    const size_t row0 = (size_t)grp * cap + (size_t)(t0 < n_tokens ? t0 : 0);
+
+    // per-wave buffer descriptors over [t0, t1): reads beyond the range return 0
+    const __amdgpu_buffer_rsrc_t rk = rsrc(kc + row0 * KROW, ntok * KROW);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(vc + row0 * VROW, ntok * VROW);
+    const __amdgpu_buffer_rsrc_t rkn = rsrc(kn + row0, ntok * 2);
+    const __amdgpu_buffer_rsrc_t rvn = rsrc(vn + row0, ntok * 2);
+    __amdgpu_buffer_rsrc_t rs = rkn, rkr = rkn;
+    if constexpr (QJL) {
+        rs = rsrc(ks + row0 * (D / 8), ntok * (D / 8));
+        rkr = rsrc(kr + row0, ntok * 2);
+    }
+
     // ------------------------------------------------------------ prologue
     for (int i = tid; i < (1 << (2 * KB)); i += NT)
         sm.ktab[i] = make_uint2(pack_hilo(Ck[i & ((1 << KB) - 1)]), pack_hilo(Ck[i >> KB]));
     for (int i = tid; i < (1 << VB); i += NT) sm.vtab[i] = pack_hilo(Cv[i]);
-    for (int i = tid; i < 8 * D; i += NT) {
+    for (int i = tid; i < NH * D; i += NT) {
         const int h = i / D, d = i % D;
         sm.u.pro.q[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
     }
@@ -194,13 +271,13 @@ __global__ __launch_bounds__(NT) void split_kernel(
         const bool proj = tid >= D;
         if (!proj || QJL) {
             const float4* row = reinterpret_cast<const float4*>((proj ? S : Rk) + (size_t)j * D);
-            float acc[8];
+            float acc[NH];
 #pragma unroll
-            for (int h = 0; h < 8; ++h) acc[h] = 0.0f;
+            for (int h = 0; h < NH; ++h) acc[h] = 0.0f;
             for (int d4 = 0; d4 < D / 4; ++d4) {
                 const float4 r4 = row[d4];
 #pragma unroll
-                for (int h = 0; h < 4 * GC; ++h) {
+                for (int h = 0; h < NH; ++h) {
                     const float* qh = sm.u.pro.q[h] + 4 * d4;
                     acc[h] = __builtin_fmaf(qh[0], r4.x, acc[h]);
                     acc[h] = __builtin_fmaf(qh[1], r4.y, acc[h]);
@@ -209,16 +286,16 @@ __global__ __launch_bounds__(NT) void split_kernel(
                 }
             }
 #pragma unroll
-            for (int h = 0; h < 8; ++h) (proj ? sm.u.pro.qp : sm.u.pro.qr)[h][j] = acc[h];
+            for (int h = 0; h < NH; ++h) (proj ? sm.u.pro.qp : sm.u.pro.qr)[h][j] = acc[h];
         }
     }
     __syncthreads();
 
-    // fixed-point scale of q_proj: |q_proj * 2^F| <= 2^30, so four balanced int8 limbs hold it
+    // fixed-point scale of q_proj: |q_proj * 2^F| < 2^30, so four balanced int8 limbs hold it
     int F = 0;
     if constexpr (QJL) {
         float mx = 0.0f;
-        for (int i = tid; i < 8 * D; i += NT) mx = fmaxf(mx, fabsf((&sm.u.pro.qp[0][0])[i]));
+        for (int i = tid; i < NH * D; i += NT) mx = fmaxf(mx, fabsf((&sm.u.pro.qp[0][0])[i]));
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
         if (lane == 0) sm.u.pro.red[wave] = mx;
@@ -230,6 +307,28 @@ __global__ __launch_bounds__(NT) void split_kernel(
         if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
         F = 30 - e;
         F = F > 100 ? 100 : F;
+        const float sc = ldexpf(1.0f, F);
+        // thread -> (head h, dim d): balanced base-256 digits of x = rint(q_proj 2^F),
+        // x = l0 + 2^8 l1 + 2^16 l2 + 2^24 l3, l_i in [-128, 127]; byte layout per lane
+        // group g and shift s: dims 32 g + s + 8 e, e = 0..3
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&sm.u.pro.limb[0][0][0][0]);
+        for (int i = tid; i < NH * D; i += NT) {
+            const int h = i / D, d = i % D;
+            int x = (int)rintf(sm.u.pro.qp[h][d] * sc);
+            const int gg = d >> 5, s = d & 7, e = (d >> 3) & 3;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int l = ((x + 128) & 255) - 128;
+                lb[(((k * NH + h) * 4 + gg) * 8 + s) * 4 + e] = (uint8_t)(l & 255);
+                x = (x - l) >> 8;
+            }
+        }
+        if (tid < NH) {
+            int64_t acc = 0;
+            for (int d = 0; d < D; ++d) acc += (int64_t)rintf(sm.u.pro.qp[tid][d] * sc);
+            sm.u.pro.sq[tid] = (float)((double)acc * (double)ldexpf(1.0f, -F));
+        }
+        __syncthreads();
     }
 
     // A operands of the key-score MFMAs (32 VGPRs): lane (i = n, g), MFMA j, VGPR r holds
@@ -244,21 +343,19 @@ __global__ __launch_bounds__(NT) void split_kernel(
         for (int r = 0; r < 4; ++r) {
             uint32_t v = 0;
             if (row_live) {
-                uint32_t hi, lo;
-                split_bf16(sm.u.pro.qr[h_row][32 * g + 4 * j + r], hi, lo);
-                v = x_row == 0 ? hi : lo;
-                v |= v << 16;
+                const float x = sm.u.pro.qr[h_row][32 * g + 4 * j + r];
+                const float hi = bf16_val(bf16_bits(x));
+                v = dup_bf16(x_row == 0 ? hi : x - hi);
             }
             qa[j][r] = v;
         }
-    // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj (dims of shift 4 jj + v),
-    // VGPR v, byte e <-> dim 32 g + 4 jj + v + 8 e.
+    // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
+    // 32 g + 4 jj + v + 8 e.
     u32x4 qj[R::NQJ][2];
-    float sq[R::HPL];  // sum_d q_proj_int[h][d] / 2^F for this lane's heads
+    float sq[R::HPL];
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) sq[i] = 0.0f;
     if constexpr (QJL) {
-        const float sc = ldexpf(1.0f, F);
 #pragma unroll
         for (int set = 0; set < R::NQJ; ++set) {
             const int h = GC == 1 ? n / 4 : n / 2;
@@ -266,109 +363,75 @@ __global__ __launch_bounds__(NT) void split_kernel(
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    uint32_t word = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        int x = 0;
-                        if (h < G) x = (int)rintf(sm.u.pro.qp[h][32 * g + 4 * jj + v + 8 * e] * sc);
-                        // balanced base-256 digits: x = l0 + 256 l1 + 65536 l2 + 2^24 l3, l_i in [-128, 127]
-                        int digit = 0;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const int l = ((x + 128) & 255) - 128;
-                            if (k == limb) digit = l;
-                            x = (x - l) >> 8;
-                        }
-                        word |= (uint32_t)(digit & 255) << (8 * e);
-                    }
-                    qj[set][jj][v] = word;
-                }
+                for (int v = 0; v < 4; ++v) qj[set][jj][v] = sm.u.pro.limb[limb][h][g][4 * jj + v];
         }
-        // per-head sums of the integer images (for the +-1 form of the signs)
 #pragma unroll
-        for (int i = 0; i < R::HPL; ++i) {
-            const int h = R::HPL * g + i;
-            double acc = 0.0;
-            if (h < G)
-                for (int d = 0; d < D; ++d) acc += (double)rintf(sm.u.pro.qp[h][d] * sc);
-            sq[i] = (float)(acc * (double)ldexpf(1.0f, -F));
-        }
+        for (int i = 0; i < R::HPL; ++i) sq[i] = sm.u.pro.sq[R::HPL * g + i];
     }
     __syncthreads();  // the prologue area is reused by the epilogue
 
-    // ---------------------------------------------------------- token range
-    int64_t len = n_tokens;
-    if (seq_lens) {
-        const int64_t l = seq_lens[b];
-        len = l < n_tokens ? (l < 0 ? 0 : l) : n_tokens;
-    }
-    int64_t start = 0;
-    if (seq_starts) {
-        const int64_t st = seq_starts[b];
-        start = st < 0 ? 0 : st;
-    }
-    int64_t r0 = (int64_t)split * tokens_per_split;
-    int64_t r1 = r0 + tokens_per_split;
-    r0 = r0 > start ? r0 : start;
-    r1 = r1 < len ? r1 : len;
-    const int64_t span = r1 > r0 ? r1 - r0 : 0;
-    const int64_t per_wave = ((span + NW - 1) / NW + BLK - 1) / BLK * BLK;
-    const int64_t t0 = r0 + (int64_t)wave * per_wave;
-    int64_t t1 = t0 + per_wave;
-    t1 = t1 < r1 ? t1 : r1;
-    const size_t row0 = (size_t)grp * cap;
-
     // per-lane softmax state (heads of this lane group) and value accumulators
-    float m_run[R::HPL], s_lane[R::HPL];
+    float m_ref[R::HPL], s_lane[R::HPL];
 #pragma unroll
-    for (int i = 0; i < R::HPL; ++i) m_run[i] = NEG_INF, s_lane[i] = 0.0f;
+    for (int i = 0; i < R::HPL; ++i) m_ref[i] = NEG_INF, s_lane[i] = 0.0f;
     f32x4 acc_v[8];
 #pragma unroll
     for (int m = 0; m < 8; ++m) acc_v[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const float c_mse = scale * LOG2E;
     const float c_qjl = scale * LOG2E * QJL_SCALE;
-    const float qfix = ldexpf(1.0f, 1 - F);  // 2 * 2^-F: sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp
+    const float qfix = ldexpf(1.0f, 1 - F);  // sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp
     uint32_t(*wt)[WT_STRIDE] = sm.wt[wave];
 
-    // value chunk of lane n: dims [8n, 8n + 8) = bits [VCH n, VCH n + VCH) of the row
-    constexpr int VCH_BYTES_MAX = VROW;
-    const int vbit0 = VCH * n;
-    const int vdw = vbit0 >> 5;                       // first dword of the chunk
-    const int vsh = vbit0 & 31;
-    const bool v2 = (vsh + VCH > 32);                 // chunk straddles two dwords (VB = 3 only)
-    (void)VCH_BYTES_MAX;
+    // lane offsets (bytes) into the per-wave buffers
+    const int ko = n * KROW + 4 * KB * g;        // key codes of token n, dims [32 g, 32 g + 32)
+    const int so = n * (D / 8) + 4 * g;          // sign bits of token n, same dims
+    const int no = 2 * n;                        // f16 norms of token n
+    const int vbit0 = VCH * n;                   // value chunk of lane n: dims [8 n, 8 n + 8)
+    // first dword read for the chunk; 3-bit chunks read two dwords, kept inside the row
+    const int vdw = VB == 3 ? ((vbit0 >> 5) < VROW / 4 - 2 ? (vbit0 >> 5) : VROW / 4 - 2) : (vbit0 >> 5);
+    const int vo = 4 * vdw + 4 * g * VROW;       // + r * VROW for token 4 g + r
+    const int vsh = vbit0 - 32 * vdw;            // in [0, 64) for VB == 3, [0, 32) otherwise
 
     struct Blk {
-        uint32_t kw[KB];     // key codes of token n, dims [32 g, 32 g + 32)
-        uint32_t sw;         // sign bits of token n, dims [32 g, 32 g + 32)
-        uint32_t kn, kr, vn; // norms (f16 bits) of token n
-        uint32_t vw[4][2];   // value codes of tokens 4 g + r, lane n's dword(s)
+        uint32_t kw[KB];      // key codes of token n, dims [32 g, 32 g + 32)
+        uint32_t sw;          // sign bits of token n, same dims
+        uint32_t kn, kr, vn;  // norms (f16 bits) of token n
+        uint32_t vw[4][2];    // value codes of tokens 4 g + r, lane n's dword(s)
     };
     auto load = [&](Blk& B, int64_t tb) {
-        const int64_t last = t1 - 1;
-        int64_t tk = tb + n;
-        tk = tk < last ? tk : last;
-        const uint32_t* kp = reinterpret_cast<const uint32_t*>(kc + (row0 + tk) * KROW) + KB * g;
-#pragma unroll
-        for (int i = 0; i < KB; ++i) B.kw[i] = kp[i];
+        const int rel = __builtin_amdgcn_readfirstlane((int)(tb - t0));  // scalar block offset
+        if constexpr (KB == 1) {
+            B.kw[0] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko, rel * KROW, 0);
+        } else if constexpr (KB == 2) {
+            const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rk, ko, rel * KROW, 0);
+            B.kw[0] = w.x, B.kw[1] = w.y;
+        } else if constexpr (KB == 3) {
+            const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rk, ko, rel * KROW, 0);
+            B.kw[0] = w.x, B.kw[1] = w.y, B.kw[2] = w.z;
+        } else {
+            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, rel * KROW, 0);
+            B.kw[0] = w.x, B.kw[1] = w.y, B.kw[2] = w.z, B.kw[3] = w.w;
+        }
         if constexpr (QJL) {
-            B.sw = reinterpret_cast<const uint32_t*>(ks + (row0 + tk) * (D / 8))[g];
-            B.kr = kr[row0 + tk];
+            B.sw = __builtin_amdgcn_raw_buffer_load_b32(rs, so, rel * (D / 8), 0);
+            B.kr = __builtin_amdgcn_raw_buffer_load_b16(rkr, no, rel * 2, 0);
         } else {
             B.sw = 0u;
             B.kr = 0u;
         }
-        B.kn = kn[row0 + tk];
-        B.vn = vn[row0 + tk];
+        B.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn, no, rel * 2, 0);
+        B.vn = __builtin_amdgcn_raw_buffer_load_b16(rvn, no, rel * 2, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            int64_t tv = tb + 4 * g + r;
-            tv = tv < last ? tv : last;
-            const uint32_t* vp = reinterpret_cast<const uint32_t*>(vc + (row0 + tv) * VROW) + vdw;
-            B.vw[r][0] = vp[0];
-            B.vw[r][1] = v2 ? vp[1] : 0u;  // never past the row: only straddling chunks read on
+            if constexpr (VB == 3) {
+                // the 24-bit chunk may straddle two dwords: read the (in-row) pair holding it
+                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + r * VROW, rel * VROW, 0);
+                B.vw[r][0] = w.x, B.vw[r][1] = w.y;
+            } else {
+                B.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + r * VROW, rel * VROW, 0);
+                B.vw[r][1] = 0u;
+            }
         }
     };
 
@@ -390,24 +453,24 @@ __global__ __launch_bounds__(NT) void split_kernel(
         // ---- QJL sums
         i32x4 acc_q[R::NQJ];
         if constexpr (QJL) {
+            u32x4 bq[2];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) bq[jj][v] = (B.sw >> (4 * jj + v)) & 0x01010101u;
 #pragma unroll
             for (int set = 0; set < R::NQJ; ++set) {
-                acc_q[set] = i32x4{0, 0, 0, 0};
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    u32x4 bq;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) bq[v] = (B.sw >> (4 * jj + v)) & 0x01010101u;
-                    acc_q[set] = mfma_i8(qj[set][jj], bq, acc_q[set]);
-                }
+                acc_q[set] = mfma_i8(qj[set][0], bq[0], i32x4{0, 0, 0, 0});
+                acc_q[set] = mfma_i8(qj[set][1], bq[1], acc_q[set]);
             }
         }
         // ---- scores (log2 domain) of token n for this lane's heads
         const bool valid = tb + n < t1;
         const float knf = tq::f16_to_f32(B.kn) * c_mse;
         const float krf = QJL ? tq::f16_to_f32(B.kr) * c_qjl : 0.0f;
-        const float vnf = tq::f16_to_f32(B.vn);
+        const float vnf = valid ? tq::f16_to_f32(B.vn) : 0.0f;
         float lg[R::HPL];
+        bool over = false;
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i) {
             float v = knf * (acc_k[2 * i] + acc_k[2 * i + 1]);
@@ -423,38 +486,32 @@ __global__ __launch_bounds__(NT) void split_kernel(
                 v = __builtin_fmaf(krf, __builtin_fmaf(qs, qfix, -sq[i]), v);
             }
             lg[i] = valid ? v : NEG_INF;
+            over |= lg[i] > m_ref[i] + LAZY_MAX;
         }
-        // ---- online softmax
-        bool grow = false;
-        float mnew[R::HPL];
-#pragma unroll
-        for (int i = 0; i < R::HPL; ++i) {
-            mnew[i] = fmaxf(m_run[i], row_max16(lg[i]));
-            grow |= mnew[i] > m_run[i];
-        }
-        if (__builtin_amdgcn_ballot_w64(grow)) {
+        // ---- online softmax with a lazily raised reference maximum
+        if (__builtin_amdgcn_ballot_w64(over)) {
 #pragma unroll
             for (int i = 0; i < R::HPL; ++i) {
-                const float a = m_run[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_run[i] - mnew[i]);
+                const float mn = fmaxf(m_ref[i], row_max16(lg[i]));
+                const float a = m_ref[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_ref[i] - mn);  // 1 if unchanged
                 s_lane[i] *= a;
 #pragma unroll
                 for (int m = 0; m < 8; ++m) {
                     acc_v[m][2 * i] *= a;
                     acc_v[m][2 * i + 1] *= a;
                 }
-                m_run[i] = mnew[i];
+                m_ref[i] = mn;
             }
         }
         uint32_t wq[R::HPL][2];
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i) {
-            const float mu = m_run[i] == NEG_INF ? 0.0f : m_run[i];
-            const float p = __builtin_amdgcn_exp2f(lg[i] - mu);
+            const float p = __builtin_amdgcn_exp2f(lg[i] - m_ref[i]);  // m_ref finite once a block is seen
             s_lane[i] += p;
-            uint32_t hi, lo;
-            split_bf16(p * vnf, hi, lo);
-            wq[i][0] = hi | (hi << 16);
-            wq[i][1] = lo | (lo << 16);
+            const float w = p * vnf;
+            const float hi = bf16_val(bf16_bits(w));
+            wq[i][0] = dup_bf16(hi);
+            wq[i][1] = dup_bf16(w - hi);
         }
         // ---- weights -> A operand of the value MFMAs (transpose through LDS)
 #pragma unroll
@@ -468,20 +525,31 @@ __global__ __launch_bounds__(NT) void split_kernel(
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
         // ---- value MFMAs: lane (n, g) supplies tokens 4 g + r, dim 8 n + m
-        uint32_t vch[4];
+        uint32_t vch[4][2];  // VB = 4: [r][0] = chunk << 2 (even codes), [r][1] = chunk >> 2 (odd codes)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if constexpr (VB == 3)
-                vch[r] = __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh);
+                vch[r][0] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh)
+                                     : B.vw[r][1] >> (vsh - 32);
             else
-                vch[r] = B.vw[r][0] >> vsh;
+                vch[r][0] = B.vw[r][0] >> vsh;
+            if constexpr (VB == 4) {
+                vch[r][1] = vch[r][0] >> 2;
+                vch[r][0] = vch[r][0] << 2;
+            }
         }
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             u32x4 bv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint32_t off = field_x<VB, 2>(&vch[r], VB * m);
+                uint32_t off;
+                if constexpr (VB == 4) {
+                    // 4 * code m = byte m/2 of (chunk << 2 if m even, chunk >> 2 if odd) & 0x3C
+                    off = (vch[r][m & 1] >> (8 * (m >> 1))) & 0x3Cu;
+                } else {
+                    off = field_x<VB, 2>(&vch[r][0], VB * m);
+                }
                 bv[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.vtab) + off);
             }
             acc_v[m] = mfma_bf16(av, bv, acc_v[m]);
@@ -521,7 +589,7 @@ __global__ __launch_bounds__(NT) void split_kernel(
 #pragma unroll
         for (int m = 0; m < 8; ++m) sm.u.epi.o[wave][h][8 * n + m] = acc_v[m][2 * i] + acc_v[m][2 * i + 1];
         if (n == 0) {
-            sm.u.epi.m[wave][h] = m_run[i];
+            sm.u.epi.m[wave][h] = m_ref[i];
             sm.u.epi.s[wave][h] = s_row[i];
         }
     }
@@ -552,41 +620,69 @@ __global__ __launch_bounds__(NT) void split_kernel(
 
 // ----------------------------------------------------------------- merge
 // One workgroup per (batch row, query head): merge the split partials (maxima in
-// the log2 domain), normalise, un-rotate by R_v.
-__global__ __launch_bounds__(D) void merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
-                                                  int n_split, const float* __restrict__ Rv,
-                                                  float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
-                                                  float* __restrict__ lse_out) {
+// the log2 domain), normalise, un-rotate by R_v.  Thread t reads R_v rows
+// k in [16 (t / 32), 16 (t / 32) + 16), columns 4 (t % 32) .. + 3, as float4.
+constexpr int MT = 256;
+__global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                                                   int n_split, const float* __restrict__ Rv,
+                                                   float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
+                                                   float* __restrict__ lse_out) {
     __shared__ float so[D];
-    __shared__ float red[2];
-    const int bh = blockIdx.x, d = threadIdx.x, lane = d & 63, wv = d >> 6;
+    __shared__ float4 part[MT / 32][D / 4];
+    __shared__ float red[MT / 64][2];
+    const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float* ml = part_ml + (size_t)bh * n_split * 2;
     float M = NEG_INF;
-    for (int k = d; k < n_split; k += D) M = fmaxf(M, ml[2 * k]);
+    for (int k = tid; k < n_split; k += MT) M = fmaxf(M, ml[2 * k]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (lane == 0) red[wv] = M;
+    if (lane == 0) red[wv][0] = M;
     __syncthreads();
-    M = fmaxf(red[0], red[1]);
-    __syncthreads();
+    M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
+    // normalised rotated output: threads (half, d) split the splits in two
+    const int d = tid & (D - 1), hf = tid >> 7;
     float o = 0.0f, s = 0.0f;
     if (M != NEG_INF) {
-        for (int k = 0; k < n_split; ++k) {
+        for (int k = hf; k < n_split; k += 2) {
             const float mk = ml[2 * k];
             const float e = mk == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
             o = __builtin_fmaf(e, part_o[((size_t)bh * n_split + k) * D + d], o);
             s = __builtin_fmaf(e, ml[2 * k + 1], s);
         }
     }
-    o = (M != NEG_INF) ? o / fmaxf(s, 1e-8f) : 0.0f;
-    if (lse_out && d == 0) lse_out[bh] = (M != NEG_INF) ? M * LN2 + logf(s) : NEG_INF;
-    so[d] = o;
+    float* po2 = reinterpret_cast<float*>(part);
+    po2[tid] = o;
+    if (d == 0) red[hf][1] = s;
     __syncthreads();
-    float a = 0.0f;
-#pragma unroll 8
-    for (int k = 0; k < D; ++k) a = __builtin_fmaf(so[k], Rv[(size_t)k * D + d], a);
-    if (out_f32) out_f32[(size_t)bh * D + d] = a;
-    if (out_bf16) out_bf16[(size_t)bh * D + d] = (uint16_t)tq::f32_to_bf16(a);
+    if (tid < D) {
+        const float sum = red[0][1] + red[1][1];
+        so[tid] = (M != NEG_INF) ? (po2[tid] + po2[tid + D]) / fmaxf(sum, 1e-8f) : 0.0f;
+        if (lse_out && tid == 0) lse_out[bh] = (M != NEG_INF) ? M * LN2 + logf(sum) : NEG_INF;
+    }
+    __syncthreads();
+    const int c4 = tid & 31, kr = tid >> 5;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4* rv4 = reinterpret_cast<const float4*>(Rv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = 16 * kr + i;
+        const float4 r = rv4[(size_t)k * (D / 4) + c4];
+        const float w = so[k];
+        acc.x = __builtin_fmaf(w, r.x, acc.x);
+        acc.y = __builtin_fmaf(w, r.y, acc.y);
+        acc.z = __builtin_fmaf(w, r.z, acc.z);
+        acc.w = __builtin_fmaf(w, r.w, acc.w);
+    }
+    part[kr][c4] = acc;
+    __syncthreads();
+    if (tid < D) {
+        const float* pf = reinterpret_cast<const float*>(part);
+        float a = 0.0f;
+#pragma unroll
+        for (int r = 0; r < MT / 32; ++r) a += pf[r * D + tid];
+        if (out_f32) out_f32[(size_t)bh * D + tid] = a;
+        if (out_bf16) out_bf16[(size_t)bh * D + tid] = (uint16_t)tq::f32_to_bf16(a);
+    }
 }
 
 struct SplitArgs {
@@ -624,18 +720,20 @@ int wgs_per_cu() {
     static int occ = 0;
     if (occ == 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, NT, 0) != hipSuccess || o < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, Cfg<GC>::NT, 0) !=
+                hipSuccess ||
+            o < 1)
             o = 1;
         occ = o;
     }
     return occ;
 }
 
-int choose_split(int groups, int64_t n_tokens, int target_wgs, int64_t* tokens_per_split) {
-    const int64_t min_per_split = (int64_t)NW * BLK * 2;  // >= two blocks per wave
+int choose_split(int groups, int64_t n_tokens, int target_wgs, int nw, int64_t* tokens_per_split) {
+    const int64_t min_per_split = (int64_t)nw * BLK * 2;  // >= two blocks per wave
     const int64_t max_split = (n_tokens + min_per_split - 1) / min_per_split;
     int64_t want = (target_wgs + groups - 1) / groups;
-    const int64_t cap_split = (MAX_RESIDENT_WGS + groups - 1) / groups;
+    const int64_t cap_split = (MAX_WGS + groups - 1) / groups;
     want = want < cap_split ? want : cap_split;
     int64_t ns = want < max_split ? want : max_split;
     if (ns < 1) ns = 1;
@@ -651,11 +749,11 @@ template <int KB, int VB, bool QJL, int GC>
 int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out, int64_t* tps_out) {
     const int target = wgs_per_cu<KB, VB, QJL, GC>() * cu_count();
     int64_t tps;
-    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, &tps);
+    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<GC>::NW, &tps);
     *n_split_out = ns;
     *tps_out = tps;
     if (a.po == nullptr) return TQ_OK;  // sizing query only
-    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(NT), 0, s, a.q, a.q_heads,
+    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<GC>::NT), 0, s, a.q, a.q_heads,
                        a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
                        a.vn, a.Rk, a.Ck, a.S, a.Cv, a.scale, tps, ns, a.po, a.pml);
     return TQ_OK;
@@ -668,8 +766,8 @@ int launch_split_g(int G, const SplitArgs& a, int groups, hipStream_t s, int* ns
     return TQ_ERR_UNSUPPORTED;
 }
 
-int dispatch(int key_bits, int value_bits, int has_qjl, int G, const SplitArgs& a, int groups, hipStream_t s,
-             int* ns, int64_t* tps) {
+int dispatch(int value_bits, int has_qjl, int G, const SplitArgs& a, int groups, hipStream_t s, int* ns,
+             int64_t* tps) {
     if (has_qjl) {
         switch (value_bits) {
             case 2: return launch_split_g<1, 2, true>(G, a, groups, s, ns, tps);
@@ -683,7 +781,6 @@ int dispatch(int key_bits, int value_bits, int has_qjl, int G, const SplitArgs& 
         case 3: return launch_split_g<3, 3, false>(G, a, groups, s, ns, tps);
         default: return launch_split_g<4, 4, false>(G, a, groups, s, ns, tps);
     }
-    (void)key_bits;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -693,9 +790,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 extern "C" size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, int kv_heads, int dim,
                                                       int64_t max_tokens) {
     if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || dim != D || max_tokens < 0) return 0;
-    // any n_tokens yields at most ceil(MAX_RESIDENT_WGS / groups) splits
+    // any n_tokens yields at most ceil(MAX_WGS / groups) splits
     const int64_t groups = (int64_t)batch * kv_heads;
-    const int bound = (int)((MAX_RESIDENT_WGS + groups - 1) / groups);
+    const int bound = (int)((MAX_WGS + groups - 1) / groups);
     return ws_layout(batch, q_heads, bound).total;
 }
 
@@ -718,7 +815,7 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     if (n_tokens > 0 && (!k_codes || !k_norms || !v_codes || !v_norms)) return TQ_ERR_INVALID_ARGUMENT;
     if (has_qjl && (!qjl || (n_tokens > 0 && (!k_signs || !k_rnorms)))) return TQ_ERR_INVALID_ARGUMENT;
     if ((k_codes && !aligned16(k_codes)) || (k_signs && !aligned16(k_signs)) || (v_codes && !aligned16(v_codes)) ||
-        !aligned16(key_rotation) || (qjl && !aligned16(qjl)))
+        !aligned16(key_rotation) || !aligned16(value_rotation) || (qjl && !aligned16(qjl)))
         return TQ_ERR_UNSUPPORTED;
     const bool combo_ok = has_qjl ? (key_bits + 1 == value_bits && value_bits >= 2 && value_bits <= 4)
                                   : (key_bits == value_bits && key_bits >= 1 && key_bits <= 4);
@@ -732,17 +829,17 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
                 v_codes, v_norms, key_rotation, key_centers, qjl, value_centers, scale, 0, 0, nullptr, nullptr};
     int n_split = 0;
     int64_t tps = 0;
-    int st = dispatch(key_bits, value_bits, has_qjl, G, a, groups, s, &n_split, &tps);  // sizing
+    int st = dispatch(value_bits, has_qjl, G, a, groups, s, &n_split, &tps);  // sizing
     if (st != TQ_OK) return st;
     const Ws w = ws_layout(batch, q_heads, n_split);
     if (workspace_bytes < w.total) return TQ_ERR_WORKSPACE;
     char* base = static_cast<char*>(workspace);
     a.po = reinterpret_cast<float*>(base + w.po);
     a.pml = reinterpret_cast<float*>(base + w.pml);
-    st = dispatch(key_bits, value_bits, has_qjl, G, a, groups, s, &n_split, &tps);
+    st = dispatch(value_bits, has_qjl, G, a, groups, s, &n_split, &tps);
     if (st != TQ_OK) return st;
     TQ_CHECK_LAUNCH();
-    hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(D), 0, s, a.po, a.pml, n_split, value_rotation,
+    hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(MT), 0, s, a.po, a.pml, n_split, value_rotation,
                        out_f32, out_bf16, lse_out);
     TQ_CHECK_LAUNCH();
     return TQ_OK;
