@@ -40,6 +40,8 @@
 
 #include "tq_common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int D = TQ_DIM;
@@ -134,6 +136,26 @@ __device__ __forceinline__ uint32_t field_x(const uint32_t* w, int pos) {
     return (w[wi] << (S - sh)) & M;
 }
 
+// (byte K of w) & mask in one VALU op (SDWA source byte select); mask lives in a VGPR
+template <int K>
+__device__ __forceinline__ uint32_t and_byte(uint32_t w, uint32_t mask) {
+    if constexpr (K == 0) {
+        return w & mask;
+    } else {
+        uint32_t r;
+        if constexpr (K == 1)
+            asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+                : "=v"(r) : "v"(mask), "v"(w));
+        else if constexpr (K == 2)
+            asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+                : "=v"(r) : "v"(mask), "v"(w));
+        else
+            asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+                : "=v"(r) : "v"(mask), "v"(w));
+        return r;
+    }
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
     const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, BUF_DW3);
@@ -183,7 +205,7 @@ struct Smem {
             float qr[NH][D];            // q R_k^T
             float qp[NH][D];            // q S^T
             uint32_t limb[4][NH][4][8]; // limb l of head h: [g][shift] -> 4 bytes (dims 32g + s + 8e)
-            float sq[NH];               // sum_d int(q_proj * 2^F) / 2^F
+            unsigned long long sqi[NH]; // sum_d int(q_proj * 2^F), two's complement
             float red[NW];
         } pro;
         struct {
@@ -254,135 +276,6 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
         rkr = rsrc(kr + row0, ntok * 2);
     }
 
-    // ------------------------------------------------------------ prologue
-    for (int i = tid; i < (1 << (2 * KB)); i += NT)
-        sm.ktab[i] = make_uint2(pack_hilo(Ck[i & ((1 << KB) - 1)]), pack_hilo(Ck[i >> KB]));
-    for (int i = tid; i < (1 << VB); i += NT) sm.vtab[i] = pack_hilo(Cv[i]);
-    for (int i = tid; i < NH * D; i += NT) {
-        const int h = i / D, d = i % D;
-        sm.u.pro.q[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
-    }
-    // rows of the weight transpose that never carry a head (GC = 1: rows 4h + 2, 4h + 3)
-    for (int i = tid; i < NW * 16 * WT_STRIDE; i += NT) (&sm.wt[0][0][0])[i] = 0u;
-    __syncthreads();
-    if (tid < 2 * D) {
-        // thread -> (matrix, output dim j): q_rot[h][j] = q[h] . R_k[j], q_proj[h][j] = q[h] . S[j]
-        const int j = tid & (D - 1);
-        const bool proj = tid >= D;
-        if (!proj || QJL) {
-            const float4* row = reinterpret_cast<const float4*>((proj ? S : Rk) + (size_t)j * D);
-            float acc[NH];
-#pragma unroll
-            for (int h = 0; h < NH; ++h) acc[h] = 0.0f;
-            for (int d4 = 0; d4 < D / 4; ++d4) {
-                const float4 r4 = row[d4];
-#pragma unroll
-                for (int h = 0; h < NH; ++h) {
-                    const float* qh = sm.u.pro.q[h] + 4 * d4;
-                    acc[h] = __builtin_fmaf(qh[0], r4.x, acc[h]);
-                    acc[h] = __builtin_fmaf(qh[1], r4.y, acc[h]);
-                    acc[h] = __builtin_fmaf(qh[2], r4.z, acc[h]);
-                    acc[h] = __builtin_fmaf(qh[3], r4.w, acc[h]);
-                }
-            }
-#pragma unroll
-            for (int h = 0; h < NH; ++h) (proj ? sm.u.pro.qp : sm.u.pro.qr)[h][j] = acc[h];
-        }
-    }
-    __syncthreads();
-
-    // fixed-point scale of q_proj: |q_proj * 2^F| < 2^30, so four balanced int8 limbs hold it
-    int F = 0;
-    if constexpr (QJL) {
-        float mx = 0.0f;
-        for (int i = tid; i < NH * D; i += NT) mx = fmaxf(mx, fabsf((&sm.u.pro.qp[0][0])[i]));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        if (lane == 0) sm.u.pro.red[wave] = mx;
-        __syncthreads();
-        mx = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm.u.pro.red[w]);
-        int e = 0;
-        if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
-        F = 30 - e;
-        F = F > 100 ? 100 : F;
-        const float sc = ldexpf(1.0f, F);
-        // thread -> (head h, dim d): balanced base-256 digits of x = rint(q_proj 2^F),
-        // x = l0 + 2^8 l1 + 2^16 l2 + 2^24 l3, l_i in [-128, 127]; byte layout per lane
-        // group g and shift s: dims 32 g + s + 8 e, e = 0..3
-        uint8_t* lb = reinterpret_cast<uint8_t*>(&sm.u.pro.limb[0][0][0][0]);
-        for (int i = tid; i < NH * D; i += NT) {
-            const int h = i / D, d = i % D;
-            int x = (int)rintf(sm.u.pro.qp[h][d] * sc);
-            const int gg = d >> 5, s = d & 7, e = (d >> 3) & 3;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int l = ((x + 128) & 255) - 128;
-                lb[(((k * NH + h) * 4 + gg) * 8 + s) * 4 + e] = (uint8_t)(l & 255);
-                x = (x - l) >> 8;
-            }
-        }
-        if (tid < NH) {
-            int64_t acc = 0;
-            for (int d = 0; d < D; ++d) acc += (int64_t)rintf(sm.u.pro.qp[tid][d] * sc);
-            sm.u.pro.sq[tid] = (float)((double)acc * (double)ldexpf(1.0f, -F));
-        }
-        __syncthreads();
-    }
-
-    // A operands of the key-score MFMAs (32 VGPRs): lane (i = n, g), MFMA j, VGPR r holds
-    // q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo codebook parts).
-    const int h_row = GC == 1 ? n / 4 : n / 2;
-    const int x_row = GC == 1 ? n % 4 : n % 2;
-    const bool row_live = x_row < 2 && h_row < G;
-    u32x4 qa[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            uint32_t v = 0;
-            if (row_live) {
-                const float x = sm.u.pro.qr[h_row][32 * g + 4 * j + r];
-                const float hi = bf16_val(bf16_bits(x));
-                v = dup_bf16(x_row == 0 ? hi : x - hi);
-            }
-            qa[j][r] = v;
-        }
-    // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
-    // 32 g + 4 jj + v + 8 e.
-    u32x4 qj[R::NQJ][2];
-    float sq[R::HPL];
-#pragma unroll
-    for (int i = 0; i < R::HPL; ++i) sq[i] = 0.0f;
-    if constexpr (QJL) {
-#pragma unroll
-        for (int set = 0; set < R::NQJ; ++set) {
-            const int h = GC == 1 ? n / 4 : n / 2;
-            const int limb = GC == 1 ? n % 4 : 2 * set + (n % 2);
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) qj[set][jj][v] = sm.u.pro.limb[limb][h][g][4 * jj + v];
-        }
-#pragma unroll
-        for (int i = 0; i < R::HPL; ++i) sq[i] = sm.u.pro.sq[R::HPL * g + i];
-    }
-    __syncthreads();  // the prologue area is reused by the epilogue
-
-    // per-lane softmax state (heads of this lane group) and value accumulators
-    float m_ref[R::HPL], s_lane[R::HPL];
-#pragma unroll
-    for (int i = 0; i < R::HPL; ++i) m_ref[i] = NEG_INF, s_lane[i] = 0.0f;
-    f32x4 acc_v[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) acc_v[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const float c_mse = scale * LOG2E;
-    const float c_qjl = scale * LOG2E * QJL_SCALE;
-    const float qfix = ldexpf(1.0f, 1 - F);  // sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp
-    uint32_t(*wt)[WT_STRIDE] = sm.wt[wave];
-
     // lane offsets (bytes) into the per-wave buffers
     const int ko = n * KROW + 4 * KB * g;        // key codes of token n, dims [32 g, 32 g + 32)
     const int so = n * (D / 8) + 4 * g;          // sign bits of token n, same dims
@@ -434,6 +327,140 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
             }
         }
     };
+
+    // ------------------------------------------------------------ prologue
+    for (int i = tid; i < (1 << (2 * KB)); i += NT)
+        sm.ktab[i] = make_uint2(pack_hilo(Ck[i & ((1 << KB) - 1)]), pack_hilo(Ck[i >> KB]));
+    for (int i = tid; i < (1 << VB); i += NT) sm.vtab[i] = pack_hilo(Cv[i]);
+    for (int i = tid; i < NH * D; i += NT) {
+        const int h = i / D, d = i % D;
+        sm.u.pro.q[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
+    }
+    // rows of the weight transpose that never carry a head (GC = 1: rows 4h + 2, 4h + 3)
+    for (int i = tid; i < NW * 16 * WT_STRIDE; i += NT) (&sm.wt[0][0][0])[i] = 0u;
+    if (tid < NH) sm.u.pro.sqi[tid] = 0ull;
+    __syncthreads();
+    {
+        // q_rot[h][j] = q[h] . R_k[j], q_proj[h][j] = q[h] . S[j]: thread -> (matrix, dim j,
+        // half of the dot product), 16 independent float4 loads, halves joined by a shuffle
+        constexpr int MATS = QJL ? 2 : 1;
+        if (tid < MATS * 2 * D) {
+            const int hf = tid & 1, j = (tid >> 1) & (D - 1), mat = tid >> 8;
+            const float4* row = reinterpret_cast<const float4*>((mat ? S : Rk) + (size_t)j * D) + 16 * hf;
+            float4 r4[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) r4[i] = row[i];
+            float acc[NH];
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const float4* qh = reinterpret_cast<const float4*>(sm.u.pro.q[h]) + 16 * hf;
+                float a = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float4 x = qh[i];
+                    a = __builtin_fmaf(x.x, r4[i].x, a);
+                    a = __builtin_fmaf(x.y, r4[i].y, a);
+                    a = __builtin_fmaf(x.z, r4[i].z, a);
+                    a = __builtin_fmaf(x.w, r4[i].w, a);
+                }
+                acc[h] = a + __shfl_xor(a, 1);
+            }
+            if (hf == 0) {
+#pragma unroll
+                for (int h = 0; h < NH; ++h) (mat ? sm.u.pro.qp : sm.u.pro.qr)[h][j] = acc[h];
+            }
+        }
+    }
+    __syncthreads();
+
+    // fixed-point scale of q_proj: |q_proj * 2^F| < 2^30, so four balanced int8 limbs hold it
+    int F = 0;
+    if constexpr (QJL) {
+        float mx = 0.0f;
+        for (int i = tid; i < NH * D; i += NT) mx = fmaxf(mx, fabsf((&sm.u.pro.qp[0][0])[i]));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if (lane == 0) sm.u.pro.red[wave] = mx;
+        __syncthreads();
+        mx = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm.u.pro.red[w]);
+        int e = 0;
+        if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
+        F = 30 - e;
+        F = F > 100 ? 100 : F;
+        const float sc = ldexpf(1.0f, F);
+        // thread -> (head h, dim d): balanced base-256 digits of x = rint(q_proj 2^F),
+        // x = l0 + 2^8 l1 + 2^16 l2 + 2^24 l3, l_i in [-128, 127]; byte layout per lane
+        // group g and shift s: dims 32 g + s + 8 e, e = 0..3
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&sm.u.pro.limb[0][0][0][0]);
+        for (int i = tid; i < NH * D; i += NT) {
+            const int h = i / D, d = i % D;
+            int x = (int)rintf(sm.u.pro.qp[h][d] * sc);
+            const int gg = d >> 5, s = d & 7, e = (d >> 3) & 3;
+            atomicAdd(&sm.u.pro.sqi[h], (unsigned long long)(long long)x);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int l = ((x + 128) & 255) - 128;
+                lb[(((k * NH + h) * 4 + gg) * 8 + s) * 4 + e] = (uint8_t)(l & 255);
+                x = (x - l) >> 8;
+            }
+        }
+        __syncthreads();
+    }
+
+    // A operands of the key-score MFMAs (32 VGPRs): lane (i = n, g), MFMA j, VGPR r holds
+    // q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo codebook parts).
+    const int h_row = GC == 1 ? n / 4 : n / 2;
+    const int x_row = GC == 1 ? n % 4 : n % 2;
+    const bool row_live = x_row < 2 && h_row < G;
+    u32x4 qa[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint32_t v = 0;
+            if (row_live) {
+                const float x = sm.u.pro.qr[h_row][32 * g + 4 * j + r];
+                const float hi = bf16_val(bf16_bits(x));
+                v = dup_bf16(x_row == 0 ? hi : x - hi);
+            }
+            qa[j][r] = v;
+        }
+    // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
+    // 32 g + 4 jj + v + 8 e.
+    u32x4 qj[R::NQJ][2];
+    float sq[R::HPL];
+#pragma unroll
+    for (int i = 0; i < R::HPL; ++i) sq[i] = 0.0f;
+    if constexpr (QJL) {
+#pragma unroll
+        for (int set = 0; set < R::NQJ; ++set) {
+            const int h = GC == 1 ? n / 4 : n / 2;
+            const int limb = GC == 1 ? n % 4 : 2 * set + (n % 2);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) qj[set][jj][v] = sm.u.pro.limb[limb][h][g][4 * jj + v];
+        }
+#pragma unroll
+        for (int i = 0; i < R::HPL; ++i)
+            sq[i] = (float)((double)(long long)sm.u.pro.sqi[R::HPL * g + i] * (double)ldexpf(1.0f, -F));
+    }
+    __syncthreads();  // the prologue area is reused by the epilogue
+
+    // per-lane softmax state (heads of this lane group) and value accumulators
+    float m_ref[R::HPL], s_lane[R::HPL];
+#pragma unroll
+    for (int i = 0; i < R::HPL; ++i) m_ref[i] = NEG_INF, s_lane[i] = 0.0f;
+    f32x4 acc_v[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) acc_v[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const float c_mse = scale * LOG2E;
+    const float c_qjl = scale * LOG2E * QJL_SCALE;
+    const float qfix = ldexpf(1.0f, 1 - F);  // sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp
+    uint32_t(*wt)[WT_STRIDE] = sm.wt[wave];
 
     auto process = [&](const Blk& B, int64_t tb) {
         // ---- key scores: 8 MFMAs over dims 32 g + 4 j + r
@@ -538,22 +565,31 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
                 vch[r][0] = vch[r][0] << 2;
             }
         }
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
+        const uint32_t m3c = __builtin_amdgcn_readfirstlane(0x3Cu);
+        auto vmfma = [&](auto mc) {
+            constexpr int m = decltype(mc)::value;
             u32x4 bv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 uint32_t off;
                 if constexpr (VB == 4) {
                     // 4 * code m = byte m/2 of (chunk << 2 if m even, chunk >> 2 if odd) & 0x3C
-                    off = (vch[r][m & 1] >> (8 * (m >> 1))) & 0x3Cu;
+                    off = and_byte<(m >> 1)>(vch[r][m & 1], m3c);
                 } else {
                     off = field_x<VB, 2>(&vch[r][0], VB * m);
                 }
                 bv[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.vtab) + off);
             }
             acc_v[m] = mfma_bf16(av, bv, acc_v[m]);
-        }
+        };
+        vmfma(std::integral_constant<int, 0>{});
+        vmfma(std::integral_constant<int, 1>{});
+        vmfma(std::integral_constant<int, 2>{});
+        vmfma(std::integral_constant<int, 3>{});
+        vmfma(std::integral_constant<int, 4>{});
+        vmfma(std::integral_constant<int, 5>{});
+        vmfma(std::integral_constant<int, 6>{});
+        vmfma(std::integral_constant<int, 7>{});
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
