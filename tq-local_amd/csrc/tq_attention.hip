@@ -66,6 +66,13 @@ constexpr float LN2 = 0.6931471805599453f;
 constexpr float QJL_SCALE = 1.2533141373155003f / D;  // sqrt(pi/2) / D
 constexpr float LAZY_MAX = 8.0f;                      // log2 headroom before the reference max is raised
 constexpr int BUF_DW3 = 0x00020000;                   // buffer descriptor word 3 (gfx9: 32-bit untyped)
+#ifndef TQ_WT_FENCE
+#define TQ_WT_FENCE 1
+#endif
+#ifndef TQ_KV_NT
+#define TQ_KV_NT 2
+#endif
+constexpr int KV_NT = TQ_KV_NT;  // buffer-load cache policy for the packed stream (2 = nt: streaming, read once)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -295,34 +302,34 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
     auto load = [&](Blk& B, int64_t tb) {
         const int rel = __builtin_amdgcn_readfirstlane((int)(tb - t0));  // scalar block offset
         if constexpr (KB == 1) {
-            B.kw[0] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko, rel * KROW, 0);
+            B.kw[0] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko, rel * KROW, KV_NT);
         } else if constexpr (KB == 2) {
-            const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rk, ko, rel * KROW, 0);
+            const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rk, ko, rel * KROW, KV_NT);
             B.kw[0] = w.x, B.kw[1] = w.y;
         } else if constexpr (KB == 3) {
-            const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rk, ko, rel * KROW, 0);
+            const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rk, ko, rel * KROW, KV_NT);
             B.kw[0] = w.x, B.kw[1] = w.y, B.kw[2] = w.z;
         } else {
-            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, rel * KROW, 0);
+            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, rel * KROW, KV_NT);
             B.kw[0] = w.x, B.kw[1] = w.y, B.kw[2] = w.z, B.kw[3] = w.w;
         }
         if constexpr (QJL) {
-            B.sw = __builtin_amdgcn_raw_buffer_load_b32(rs, so, rel * (D / 8), 0);
-            B.kr = __builtin_amdgcn_raw_buffer_load_b16(rkr, no, rel * 2, 0);
+            B.sw = __builtin_amdgcn_raw_buffer_load_b32(rs, so, rel * (D / 8), KV_NT);
+            B.kr = __builtin_amdgcn_raw_buffer_load_b16(rkr, no, rel * 2, KV_NT);
         } else {
             B.sw = 0u;
             B.kr = 0u;
         }
-        B.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn, no, rel * 2, 0);
-        B.vn = __builtin_amdgcn_raw_buffer_load_b16(rvn, no, rel * 2, 0);
+        B.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn, no, rel * 2, KV_NT);
+        B.vn = __builtin_amdgcn_raw_buffer_load_b16(rvn, no, rel * 2, KV_NT);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if constexpr (VB == 3) {
                 // the 24-bit chunk may straddle two dwords: read the (in-row) pair holding it
-                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + r * VROW, rel * VROW, 0);
+                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + r * VROW, rel * VROW, KV_NT);
                 B.vw[r][0] = w.x, B.vw[r][1] = w.y;
             } else {
-                B.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + r * VROW, rel * VROW, 0);
+                B.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + r * VROW, rel * VROW, KV_NT);
                 B.vw[r][1] = 0u;
             }
         }
@@ -339,17 +346,22 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
     // rows of the weight transpose that never carry a head (GC = 1: rows 4h + 2, 4h + 3)
     for (int i = tid; i < NW * 16 * WT_STRIDE; i += NT) (&sm.wt[0][0][0])[i] = 0u;
     if (tid < NH) sm.u.pro.sqi[tid] = 0ull;
+    // q_rot[h][j] = q[h] . R_k[j], q_proj[h][j] = q[h] . S[j]: thread -> (matrix, dim j,
+    // half of the dot product), 16 independent float4 loads issued in the same round as
+    // the q / codebook reads above; halves joined by a shuffle
+    constexpr int MATS = QJL ? 2 : 1;
+    const bool mv_thread = tid < MATS * 2 * D;
+    const int mv_hf = tid & 1, mv_j = (tid >> 1) & (D - 1), mv_mat = tid >> 8;
+    float4 r4[16];
+    if (mv_thread) {
+        const float4* row = reinterpret_cast<const float4*>((mv_mat ? S : Rk) + (size_t)mv_j * D) + 16 * mv_hf;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r4[i] = row[i];
+    }
     __syncthreads();
     {
-        // q_rot[h][j] = q[h] . R_k[j], q_proj[h][j] = q[h] . S[j]: thread -> (matrix, dim j,
-        // half of the dot product), 16 independent float4 loads, halves joined by a shuffle
-        constexpr int MATS = QJL ? 2 : 1;
-        if (tid < MATS * 2 * D) {
-            const int hf = tid & 1, j = (tid >> 1) & (D - 1), mat = tid >> 8;
-            const float4* row = reinterpret_cast<const float4*>((mat ? S : Rk) + (size_t)j * D) + 16 * hf;
-            float4 r4[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) r4[i] = row[i];
+        if (mv_thread) {
+            const int hf = mv_hf, j = mv_j, mat = mv_mat;
             float acc[NH];
 #pragma unroll
             for (int h = 0; h < NH; ++h) {
@@ -547,9 +559,11 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
             wt[R::row(h, 0)][n] = wq[i][0];
             wt[R::row(h, 1)][n] = wq[i][1];
         }
+#if TQ_WT_FENCE
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#endif
         const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
         // ---- value MFMAs: lane (n, g) supplies tokens 4 g + r, dim 8 n + m
         uint32_t vch[4][2];  // VB = 4: [r][0] = chunk << 2 (even codes), [r][1] = chunk >> 2 (odd codes)
@@ -590,9 +604,11 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
         vmfma(std::integral_constant<int, 5>{});
         vmfma(std::integral_constant<int, 6>{});
         vmfma(std::integral_constant<int, 7>{});
+#if TQ_WT_FENCE
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#endif
     };
 
     if (t0 < t1) {
