@@ -120,6 +120,10 @@ def main() -> int:
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--no-qjl", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch every layer from Python instead of a HIP graph")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed region, run a plain elementwise copy of one layer's packed size "
+                         "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -181,26 +185,77 @@ def main() -> int:
         for li in range(args.layers):
             attn(li)
     torch.cuda.synchronize()
-
     stream = torch.cuda.current_stream(dev)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps * args.layers)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps * args.layers)]
+
+    # per-call HIP events on the launch stream (eager calls; each brackets the split
+    # and merge kernels of one tq_decode_attention call)
+    n_ev = min(args.steps, 10) * args.layers
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    torch.cuda.synchronize()
+    for i in range(n_ev):
+        starts[i].record(stream)
+        attn(i % args.layers)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    eager_call_us = statistics.fmean(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))
+
+    # one decode step = all layers, captured once in a HIP graph and replayed, so the
+    # timed region holds only GPU work (no Python dispatch gaps between layers)
+    graph = None
+    if not args.eager:
+        ref = [attn(li) for li in range(args.layers)]
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            outs = [attn(li) for li in range(args.layers)]
+        for rep in range(2):
+            graph.replay()
+            torch.cuda.synchronize()
+            bad = [li for li in range(args.layers) if not torch.equal(outs[li], ref[li])]
+            if bad:
+                print(f"[bench] graph replay {rep} differs from eager on layers {bad}", file=sys.stderr)
+                return 1
+            attn(0)  # eager work between replays
+        torch.cuda.synchronize()
+
+    def step():
+        if graph is not None:
+            graph.replay()
+        else:
+            for li in range(args.layers):
+                attn(li)
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    i = 0
+    e0.record(stream)
     for _ in range(args.steps):
-        for li in range(args.layers):
-            starts[i].record(stream)
-            attn(li)
-            ends[i].record(stream)
-            i += 1
+        step()
+    e1.record(stream)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    call_us = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
-    avg_us = statistics.fmean(call_us)
+    step_us = e0.elapsed_time(e1) * 1e3 / args.steps
+    avg_us = step_us / args.layers
     ms_per_step = elapsed * 1e3 / args.steps
     value = layer_bytes * args.layers * args.steps / elapsed / 1e9
     achieved = layer_bytes / (avg_us * 1e-6) / 1e9
+
+    copy_cal = None
+    if args.copy_calibration:
+        # torch.neg over fp32: one read and one write of exactly `layer_bytes` each
+        src = torch.randn(layer_bytes // 4, device=dev)
+        dst = torch.empty_like(src)
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.neg(src, out=dst)
+        c0.record(stream)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        copy_cal = {"kernel": "torch.neg fp32 (elementwise)", "read_bytes": src.numel() * 4,
+                    "write_bytes": dst.numel() * 4, "us": round(c0.elapsed_time(c1) * 1e3 / 3, 2)}
+        del src, dst
 
     # prefill quantizer: bytes = bf16 K+V in + packed out; flops = 2 D^2 per matvec (4 for Q_prod K + V)
     q_s = statistics.median(q_ms) * 1e-3
@@ -217,11 +272,12 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "us_per_layer": round(avg_us, 3),
+        "launch": "eager" if graph is None else "hip_graph",
         "hbm_peak_frac": round(value / HBM_PEAK_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "u8 codes; bf16 hi/lo + int8 MFMA, fp32 accumulate",
         "data": "synthetic",
         "config": {
             "workload": (f"BASELINE config 2: decode attention over {args.layers} independently seeded packed "
@@ -241,7 +297,10 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "tq_decode_attention (prepare + split + merge launches of one call), HIP events per call",
+            "kernel": ("tq_decode_attention = split_kernel + merge_kernel; duration = HIP events around the "
+                       "timed graph replays on the launch stream / (steps x layers)"),
+            "us_per_call": round(avg_us, 3),
+            "eager_us_per_call": round(eager_call_us, 3),
         },
         "prefill_quantizer": {
             "ms_per_layer": round(q_s * 1e3, 3),
@@ -250,6 +309,8 @@ def main() -> int:
             "fp32_valu_peak_tflops": VALU_FP32_PEAK_TFLOPS,
         },
     }
+    if copy_cal is not None:
+        line["copy_calibration"] = copy_cal
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bits)
     print(json.dumps(line))

@@ -45,17 +45,21 @@
 namespace {
 
 constexpr int D = TQ_DIM;
-// waves per split workgroup: 3 per SIMD where the registers allow it (at most 4 query
-// heads per KV head), 2 per SIMD otherwise
+// waves per split workgroup (one workgroup per CU): 4 per SIMD for the paired 4-bit value
+// layout (<= 128 VGPRs), 3 per SIMD for the other layouts with at most 4 query heads per KV
+// head, 2 per SIMD with 5..8
+#ifndef TQ_ATTN_WAVES_P
+#define TQ_ATTN_WAVES_P 16
+#endif
 #ifndef TQ_ATTN_WAVES_G4
 #define TQ_ATTN_WAVES_G4 12
 #endif
 #ifndef TQ_ATTN_WAVES_G8
 #define TQ_ATTN_WAVES_G8 8
 #endif
-template <int GC>
+template <int VB, int GC>
 struct Cfg {
-    static constexpr int NW = GC == 1 ? TQ_ATTN_WAVES_G4 : TQ_ATTN_WAVES_G8;
+    static constexpr int NW = GC == 1 ? (VB == 4 ? TQ_ATTN_WAVES_P : TQ_ATTN_WAVES_G4) : TQ_ATTN_WAVES_G8;
     static constexpr int NT = NW * 64;
 };
 constexpr int BLK = 16;        // tokens per block (MFMA N)
@@ -199,20 +203,37 @@ struct Rows {
     __host__ __device__ static constexpr int row(int h, int x) { return GC == 1 ? 4 * h + x : 2 * h + x; }
 };
 
+// Value MFMA layouts.  Generic: rows (head, w hi|lo), columns = 16 dims, k-slots = 16 tokens
+// x (Cv hi, Cv lo), one 4-byte table lookup per code.  Paired (4-bit values, at most 4
+// heads): rows (head, dim parity p, w hi|lo) fill all 16 rows, columns = 16 pairs of
+// adjacent dims, k-slots = 8 tokens x parity x (Cv hi, Cv lo); one 8-byte lookup per code
+// byte returns both dims of a pair, and the A operand is zero where the parities differ.
+template <int VB, int GC>
+constexpr bool PAIRED = GC == 1 && VB == 4;
+constexpr int VCOPIES = 32;      // lane-private copies of the 256-entry pair table (bank pair per lane)
+constexpr int WT_STRIDE_P = 36;  // dwords per weight row in the paired layout (32 slots + bank spread)
+
 template <int KB, int VB, bool QJL, int GC>
 struct Smem {
     static constexpr int NH = 4 * GC;
-    static constexpr int NW = Cfg<GC>::NW;
+    static constexpr int NW = Cfg<VB, GC>::NW;
+    static constexpr bool PV = PAIRED<VB, GC>;
+    static constexpr int WTS = PV ? WT_STRIDE_P : WT_STRIDE;
+    // both lookup tables sit below 64 KB, so their base folds into the LDS instruction's offset
     uint2 ktab[1 << (2 * KB)];          // (Ck hi|lo of c0, Ck hi|lo of c1) per pair of key codes
-    uint32_t vtab[1 << VB];             // Cv hi|lo per value code
-    uint32_t wt[NW][16][WT_STRIDE];     // per-wave transpose of the softmax weights
+    // paired: (Cv hi|lo of the low nibble, Cv hi|lo of the high nibble) per code byte, entry e
+    // of copy c at byte 256 e + 8 c from the table base
+    uint2 vtab2[PV ? 256 : 1][PV ? VCOPIES : 1];
+    uint32_t vtab[1 << VB];             // Cv hi|lo per value code (generic layout)
+    uint32_t wt[NW][16][WTS];           // per-wave transpose of the softmax weights
+    uint32_t limb[4][NH][4][8];         // QJL A operand: limb l of head h, [g][shift] -> 4 bytes (dims 32g + s + 8e)
     union {
         struct {
             float q[NH][D];
             float qr[NH][D];            // q R_k^T
             float qp[NH][D];            // q S^T
-            uint32_t limb[4][NH][4][8]; // limb l of head h: [g][shift] -> 4 bytes (dims 32g + s + 8e)
-            unsigned long long sqi[NH]; // sum_d int(q_proj * 2^F), two's complement
+            double sqd[2 * NH];         // sum of int(q_proj * 2^F) over each half (64 dims) of a head
+            uint32_t ksrc[16];          // Ck hi|lo per key code
             float red[NW];
         } pro;
         struct {
@@ -224,7 +245,7 @@ struct Smem {
 };
 
 template <int KB, int VB, bool QJL, int GC>
-__global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
+__global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
@@ -233,8 +254,8 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
     using Sm = Smem<KB, VB, QJL, GC>;
     using R = Rows<GC>;
-    constexpr int NW = Cfg<GC>::NW;
-    constexpr int NT = Cfg<GC>::NT;
+    constexpr int NW = Cfg<VB, GC>::NW;
+    constexpr int NT = Cfg<VB, GC>::NT;
     constexpr int NH = R::NH;
     constexpr int KROW = D * KB / 8;  // bytes per key row
     constexpr int VROW = D * VB / 8;  // bytes per value row
@@ -290,14 +311,14 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
     const int vbit0 = VCH * n;                   // value chunk of lane n: dims [8 n, 8 n + 8)
     // first dword read for the chunk; 3-bit chunks read two dwords, kept inside the row
     const int vdw = VB == 3 ? ((vbit0 >> 5) < VROW / 4 - 2 ? (vbit0 >> 5) : VROW / 4 - 2) : (vbit0 >> 5);
-    const int vo = 4 * vdw + 4 * g * VROW;       // + r * VROW for token 4 g + r
+    const int vo = 4 * vdw + g * VROW;           // + 4 r VROW for token 4 r + g (each load: 4 whole rows)
     const int vsh = vbit0 - 32 * vdw;            // in [0, 64) for VB == 3, [0, 32) otherwise
 
     struct Blk {
         uint32_t kw[KB];      // key codes of token n, dims [32 g, 32 g + 32)
         uint32_t sw;          // sign bits of token n, same dims
         uint32_t kn, kr, vn;  // norms (f16 bits) of token n
-        uint32_t vw[4][2];    // value codes of tokens 4 g + r, lane n's dword(s)
+        uint32_t vw[4][2];    // value codes of tokens 4 r + g, lane n's dword(s)
     };
     auto load = [&](Blk& B, int64_t tb) {
         const int rel = __builtin_amdgcn_readfirstlane((int)(tb - t0));  // scalar block offset
@@ -326,29 +347,28 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
         for (int r = 0; r < 4; ++r) {
             if constexpr (VB == 3) {
                 // the 24-bit chunk may straddle two dwords: read the (in-row) pair holding it
-                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + r * VROW, rel * VROW, KV_NT);
+                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + 4 * r * VROW, rel * VROW, KV_NT);
                 B.vw[r][0] = w.x, B.vw[r][1] = w.y;
             } else {
-                B.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + r * VROW, rel * VROW, KV_NT);
+                B.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + 4 * r * VROW, rel * VROW, KV_NT);
                 B.vw[r][1] = 0u;
             }
         }
     };
 
     // ------------------------------------------------------------ prologue
-    for (int i = tid; i < (1 << (2 * KB)); i += NT)
-        sm.ktab[i] = make_uint2(pack_hilo(Ck[i & ((1 << KB) - 1)]), pack_hilo(Ck[i >> KB]));
-    for (int i = tid; i < (1 << VB); i += NT) sm.vtab[i] = pack_hilo(Cv[i]);
+    // round 1: every global read of the prologue is issued before the first barrier (one
+    // memory round trip): codebooks (hi|lo), q, and the R_k / S rows of the mat-vec threads
+    if (tid < (1 << KB)) sm.u.pro.ksrc[tid] = pack_hilo(Ck[tid]);
+    if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = pack_hilo(Cv[tid - 64]);
     for (int i = tid; i < NH * D; i += NT) {
         const int h = i / D, d = i % D;
         sm.u.pro.q[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
     }
-    // rows of the weight transpose that never carry a head (GC = 1: rows 4h + 2, 4h + 3)
-    for (int i = tid; i < NW * 16 * WT_STRIDE; i += NT) (&sm.wt[0][0][0])[i] = 0u;
-    if (tid < NH) sm.u.pro.sqi[tid] = 0ull;
+    // zero slots of the weight transpose (never written by the loop)
+    for (int i = tid; i < NW * 16 * Sm::WTS; i += NT) (&sm.wt[0][0][0])[i] = 0u;
     // q_rot[h][j] = q[h] . R_k[j], q_proj[h][j] = q[h] . S[j]: thread -> (matrix, dim j,
-    // half of the dot product), 16 independent float4 loads issued in the same round as
-    // the q / codebook reads above; halves joined by a shuffle
+    // half of the dot product), 16 independent float4 loads; halves joined by a shuffle
     constexpr int MATS = QJL ? 2 : 1;
     const bool mv_thread = tid < MATS * 2 * D;
     const int mv_hf = tid & 1, mv_j = (tid >> 1) & (D - 1), mv_mat = tid >> 8;
@@ -359,6 +379,15 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
         for (int i = 0; i < 16; ++i) r4[i] = row[i];
     }
     __syncthreads();
+    // round 2 (LDS only): pair tables expanded from the codebooks, then the mat-vecs
+    for (int i = tid; i < (1 << (2 * KB)); i += NT)
+        sm.ktab[i] = make_uint2(sm.u.pro.ksrc[i & ((1 << KB) - 1)], sm.u.pro.ksrc[i >> KB]);
+    if constexpr (Sm::PV) {
+        for (int i = tid; i < 256 * VCOPIES; i += NT) {
+            const int e = i / VCOPIES;
+            (&sm.vtab2[0][0])[i] = make_uint2(sm.vtab[e & 15], sm.vtab[e >> 4]);
+        }
+    }
     {
         if (mv_thread) {
             const int hf = mv_hf, j = mv_j, mat = mv_mat;
@@ -405,12 +434,17 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
         // thread -> (head h, dim d): balanced base-256 digits of x = rint(q_proj 2^F),
         // x = l0 + 2^8 l1 + 2^16 l2 + 2^24 l3, l_i in [-128, 127]; byte layout per lane
         // group g and shift s: dims 32 g + s + 8 e, e = 0..3
-        uint8_t* lb = reinterpret_cast<uint8_t*>(&sm.u.pro.limb[0][0][0][0]);
+        // sum_d x per head: 64 consecutive elements (one wave, one head) summed exactly in
+        // fp64 (|x| < 2^30, 64 terms), the NH * D / 64 wave sums combined after the barrier
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&sm.limb[0][0][0][0]);
         for (int i = tid; i < NH * D; i += NT) {
             const int h = i / D, d = i % D;
             int x = (int)rintf(sm.u.pro.qp[h][d] * sc);
+            double xs = (double)x;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) xs += __shfl_xor(xs, off);
+            if (lane == 0) sm.u.pro.sqd[i >> 6] = xs;
             const int gg = d >> 5, s = d & 7, e = (d >> 3) & 3;
-            atomicAdd(&sm.u.pro.sqi[h], (unsigned long long)(long long)x);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int l = ((x + 128) & 255) - 128;
@@ -453,11 +487,12 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) qj[set][jj][v] = sm.u.pro.limb[limb][h][g][4 * jj + v];
+                for (int v = 0; v < 4; ++v) qj[set][jj][v] = sm.limb[limb][h][g][4 * jj + v];
         }
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i)
-            sq[i] = (float)((double)(long long)sm.u.pro.sqi[R::HPL * g + i] * (double)ldexpf(1.0f, -F));
+            sq[i] = (float)((sm.u.pro.sqd[2 * (R::HPL * g + i)] + sm.u.pro.sqd[2 * (R::HPL * g + i) + 1]) *
+                            (double)ldexpf(1.0f, -F));
     }
     __syncthreads();  // the prologue area is reused by the epilogue
 
@@ -465,14 +500,22 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
     float m_ref[R::HPL], s_lane[R::HPL];
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) m_ref[i] = NEG_INF, s_lane[i] = 0.0f;
-    f32x4 acc_v[8];
+    constexpr bool PV = Sm::PV;
+    constexpr int NACC = PV ? 4 : 8;  // value accumulators: column groups of 16 pairs / 16 dims
+    f32x4 acc_v[NACC];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) acc_v[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < NACC; ++m) acc_v[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const float c_mse = scale * LOG2E;
     const float c_qjl = scale * LOG2E * QJL_SCALE;
     const float qfix = ldexpf(1.0f, 1 - F);  // sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp
-    uint32_t(*wt)[WT_STRIDE] = sm.wt[wave];
+    uint32_t(*wt)[Sm::WTS] = sm.wt[wave];
+    // generic layout: token 4 r + g sits at k-slot pair 4 g + r
+    const int wslot = 4 * (n & 3) + (n >> 2);
+    // paired layout: token n = 8 u + 4 s + k (u: MFMA half, k: lane group, s: which of its
+    // two tokens) -> dwords 4 (4 u + k) + 2 s + p of rows (head, p, x)
+    const int pslot = 4 * (4 * (n >> 3) + (n & 3)) + 2 * ((n >> 2) & 1);
+    const uint32_t plane = 8u * (uint32_t)(lane & (VCOPIES - 1));  // copy of the pair table
 
     auto process = [&](const Blk& B, int64_t tb) {
         // ---- key scores: 8 MFMAs over dims 32 g + 4 j + r
@@ -534,10 +577,15 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
                 const float mn = fmaxf(m_ref[i], row_max16(lg[i]));
                 const float a = m_ref[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_ref[i] - mn);  // 1 if unchanged
                 s_lane[i] *= a;
+                if constexpr (PV) {
 #pragma unroll
-                for (int m = 0; m < 8; ++m) {
-                    acc_v[m][2 * i] *= a;
-                    acc_v[m][2 * i + 1] *= a;
+                    for (int m = 0; m < NACC; ++m) acc_v[m] *= a;  // all four rows are this lane's head
+                } else {
+#pragma unroll
+                    for (int m = 0; m < NACC; ++m) {
+                        acc_v[m][2 * i] *= a;
+                        acc_v[m][2 * i + 1] *= a;
+                    }
                 }
                 m_ref[i] = mn;
             }
@@ -553,57 +601,85 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
             wq[i][1] = dup_bf16(w - hi);
         }
         // ---- weights -> A operand of the value MFMAs (transpose through LDS)
+        if constexpr (PV) {
+            // rows 4 h + 2 p + x: this lane's head is g; the zero slots are never written
+            wt[4 * g + 0][pslot] = wq[0][0];
+            wt[4 * g + 1][pslot] = wq[0][1];
+            wt[4 * g + 2][pslot + 1] = wq[0][0];
+            wt[4 * g + 3][pslot + 1] = wq[0][1];
+        } else {
 #pragma unroll
-        for (int i = 0; i < R::HPL; ++i) {
-            const int h = R::HPL * g + i;
-            wt[R::row(h, 0)][n] = wq[i][0];
-            wt[R::row(h, 1)][n] = wq[i][1];
+            for (int i = 0; i < R::HPL; ++i) {
+                const int h = R::HPL * g + i;
+                wt[R::row(h, 0)][wslot] = wq[i][0];
+                wt[R::row(h, 1)][wslot] = wq[i][1];
+            }
         }
 #if TQ_WT_FENCE
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #endif
-        const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
-        // ---- value MFMAs: lane (n, g) supplies tokens 4 g + r, dim 8 n + m
-        uint32_t vch[4][2];  // VB = 4: [r][0] = chunk << 2 (even codes), [r][1] = chunk >> 2 (odd codes)
+        if constexpr (PV) {
+            // ---- value MFMAs, paired: lane (c = n, k = g) supplies tokens 8 u + 4 s + g, pair
+            // column c of group m = code byte m of dword c (dims 8 c + 2 m, 8 c + 2 m + 1)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if constexpr (VB == 3)
-                vch[r][0] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh)
-                                     : B.vw[r][1] >> (vsh - 32);
-            else
-                vch[r][0] = B.vw[r][0] >> vsh;
-            if constexpr (VB == 4) {
-                vch[r][1] = vch[r][0] >> 2;
-                vch[r][0] = vch[r][0] << 2;
+            for (int u = 0; u < 2; ++u) {
+                const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * (4 * u + g)]);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    // LDS byte offset 256 * byte m + plane in one v_perm: [plane, byte m, 0, 0]
+                    constexpr uint32_t SEL_LO = 0x0C0C0000u;
+                    const uint32_t sel = SEL_LO | ((4u + (uint32_t)m) << 8);
+                    const uint32_t o0 = __builtin_amdgcn_perm(B.vw[2 * u][0], plane, sel);
+                    const uint32_t o1 = __builtin_amdgcn_perm(B.vw[2 * u + 1][0], plane, sel);
+                    const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
+                    const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
+                    acc_v[m] = mfma_bf16(av, u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
+                }
             }
-        }
-        const uint32_t m3c = __builtin_amdgcn_readfirstlane(0x3Cu);
-        auto vmfma = [&](auto mc) {
-            constexpr int m = decltype(mc)::value;
-            u32x4 bv;
+        } else {
+            const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
+            // ---- value MFMAs: lane (n, g) supplies tokens 4 r + g (k-slots 8 g + 2 r + y), dim 8 n + m
+            uint32_t vch[4][2];  // VB = 4: [r][0] = chunk << 2 (even codes), [r][1] = chunk >> 2 (odd codes)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                uint32_t off;
+                if constexpr (VB == 3)
+                    vch[r][0] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh)
+                                         : B.vw[r][1] >> (vsh - 32);
+                else
+                    vch[r][0] = B.vw[r][0] >> vsh;
                 if constexpr (VB == 4) {
-                    // 4 * code m = byte m/2 of (chunk << 2 if m even, chunk >> 2 if odd) & 0x3C
-                    off = and_byte<(m >> 1)>(vch[r][m & 1], m3c);
-                } else {
-                    off = field_x<VB, 2>(&vch[r][0], VB * m);
+                    vch[r][1] = vch[r][0] >> 2;
+                    vch[r][0] = vch[r][0] << 2;
                 }
-                bv[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.vtab) + off);
             }
-            acc_v[m] = mfma_bf16(av, bv, acc_v[m]);
-        };
-        vmfma(std::integral_constant<int, 0>{});
-        vmfma(std::integral_constant<int, 1>{});
-        vmfma(std::integral_constant<int, 2>{});
-        vmfma(std::integral_constant<int, 3>{});
-        vmfma(std::integral_constant<int, 4>{});
-        vmfma(std::integral_constant<int, 5>{});
-        vmfma(std::integral_constant<int, 6>{});
-        vmfma(std::integral_constant<int, 7>{});
+            const uint32_t m3c = __builtin_amdgcn_readfirstlane(0x3Cu);
+            auto vmfma = [&](auto mc) {
+                constexpr int m = decltype(mc)::value;
+                u32x4 bv;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    uint32_t off;
+                    if constexpr (VB == 4) {
+                        // 4 * code m = byte m/2 of (chunk << 2 if m even, chunk >> 2 if odd) & 0x3C
+                        off = and_byte<(m >> 1)>(vch[r][m & 1], m3c);
+                    } else {
+                        off = field_x<VB, 2>(&vch[r][0], VB * m);
+                    }
+                    bv[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.vtab) + off);
+                }
+                acc_v[m] = mfma_bf16(av, bv, acc_v[m]);
+            };
+            vmfma(std::integral_constant<int, 0>{});
+            vmfma(std::integral_constant<int, 1>{});
+            vmfma(std::integral_constant<int, 2>{});
+            vmfma(std::integral_constant<int, 3>{});
+            vmfma(std::integral_constant<int, 4>{});
+            vmfma(std::integral_constant<int, 5>{});
+            vmfma(std::integral_constant<int, 6>{});
+            vmfma(std::integral_constant<int, 7>{});
+        }
 #if TQ_WT_FENCE
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -634,12 +710,21 @@ __global__ __launch_bounds__(Cfg<GC>::NT) void split_kernel(
     float s_row[R::HPL];
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) s_row[i] = row_sum16(s_lane[i]);
-    // lane (n, g): dims 8 n + m of heads R::HPL g + i
+    // generic: lane (n, g) holds dims 8 n + m of heads R::HPL g + i; paired: lane (n, g) holds
+    // head g, dims 8 n + 2 m + p in rows (p, x) = (r >> 1, r & 1)
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) {
         const int h = R::HPL * g + i;
+        if constexpr (PV) {
 #pragma unroll
-        for (int m = 0; m < 8; ++m) sm.u.epi.o[wave][h][8 * n + m] = acc_v[m][2 * i] + acc_v[m][2 * i + 1];
+            for (int m = 0; m < NACC; ++m) {
+                sm.u.epi.o[wave][h][8 * n + 2 * m] = acc_v[m][0] + acc_v[m][1];
+                sm.u.epi.o[wave][h][8 * n + 2 * m + 1] = acc_v[m][2] + acc_v[m][3];
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < NACC; ++m) sm.u.epi.o[wave][h][8 * n + m] = acc_v[m][2 * i] + acc_v[m][2 * i + 1];
+        }
         if (n == 0) {
             sm.u.epi.m[wave][h] = m_ref[i];
             sm.u.epi.s[wave][h] = s_row[i];
@@ -772,7 +857,7 @@ int wgs_per_cu() {
     static int occ = 0;
     if (occ == 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, Cfg<GC>::NT, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, Cfg<VB, GC>::NT, 0) !=
                 hipSuccess ||
             o < 1)
             o = 1;
@@ -801,11 +886,11 @@ template <int KB, int VB, bool QJL, int GC>
 int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out, int64_t* tps_out) {
     const int target = wgs_per_cu<KB, VB, QJL, GC>() * cu_count();
     int64_t tps;
-    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<GC>::NW, &tps);
+    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC>::NW, &tps);
     *n_split_out = ns;
     *tps_out = tps;
     if (a.po == nullptr) return TQ_OK;  // sizing query only
-    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<GC>::NT), 0, s, a.q, a.q_heads,
+    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC>::NT), 0, s, a.q, a.q_heads,
                        a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
                        a.vn, a.Rk, a.Ck, a.S, a.Cv, a.scale, tps, ns, a.po, a.pml);
     return TQ_OK;
