@@ -63,6 +63,10 @@ struct Cfg {
     static constexpr int NT = NW * 64;
 };
 constexpr int BLK = 16;        // tokens per block (MFMA N)
+// lane-private copies of the key pair table: 32 for the 64-entry (3-bit) table; the 256-entry
+// 4-bit table gets 8 where the paired value table already takes 64 KB of LDS
+template <int KB, bool PV>
+constexpr int KCOPIES = KB <= 3 ? 32 : (PV ? 8 : 32);
 constexpr int WT_STRIDE = 20;  // dwords per row of the weight-transpose buffer (bank spread)
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LOG2E = 1.4426950408889634f;
@@ -173,8 +177,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
 }
 
 struct Ws {
-    size_t po, pml, total;
+    size_t po, pml, img, total;
 };
+
+// Per-group q-side image written by prep_kernel and read by every split workgroup of the
+// group: the register contents of the key-score and QJL A operands for one wave (lane-major,
+// one 16-byte load per lane and slot), the per-head QJL offsets and the fixed-point scale.
+constexpr int IMG_QA = 0;                   // [8 j][64 lanes][4]  key-score A operand
+constexpr int IMG_QJ = IMG_QA + 8 * 64 * 4;  // [set][2 jj][64 lanes][4]  QJL A operand (int8 limbs)
+constexpr int IMG_SQ = IMG_QJ + 2 * 2 * 64 * 4;  // [8 heads] sum_d q_proj (fixed-point, as float)
+constexpr int IMG_QFIX = IMG_SQ + 8;         // 2^(1 - F)
+constexpr int IMG_DW = IMG_QFIX + 8;         // dwords per group (a multiple of 4)
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -183,13 +196,16 @@ Ws ws_layout(int batch, int q_heads, int n_split) {
     const size_t bh = (size_t)batch * q_heads;
     w.po = 0;
     w.pml = align256(w.po + bh * (size_t)n_split * D * sizeof(float));
-    w.total = align256(w.pml + bh * (size_t)n_split * 2 * sizeof(float));
+    w.img = align256(w.pml + bh * (size_t)n_split * 2 * sizeof(float));
+    const size_t groups = (size_t)batch * q_heads;  // >= batch * kv_heads
+    w.total = align256(w.img + groups * IMG_DW * sizeof(uint32_t));
     return w;
 }
 
 // Upper bound on splits per group for any token count: the grid never exceeds
 // MAX_WGS workgroups.
 constexpr int MAX_WGS = 1024;
+constexpr int MT = 256;  // threads per head in the merge
 
 // ------------------------------------------------------------------ split kernel
 // GC = 1: at most 4 query heads per KV head; row 4h + x of every MFMA belongs to
@@ -219,38 +235,245 @@ struct Smem {
     static constexpr int NW = Cfg<VB, GC>::NW;
     static constexpr bool PV = PAIRED<VB, GC>;
     static constexpr int WTS = PV ? WT_STRIDE_P : WT_STRIDE;
-    // both lookup tables sit below 64 KB, so their base folds into the LDS instruction's offset
-    uint2 ktab[1 << (2 * KB)];          // (Ck hi|lo of c0, Ck hi|lo of c1) per pair of key codes
+    // both lookup tables sit below 64 KB, so their base folds into the LDS instruction's offset.
+    // (Ck hi|lo of c0, Ck hi|lo of c1) per pair of key codes; KC lane-private copies, entry e of
+    // copy c at byte 8 (KC e + c), so the lanes of a 32-lane LDS pass use distinct bank pairs
+    static constexpr int KC = KCOPIES<KB, PV>;
+    uint2 ktab[1 << (2 * KB)][KC];
     // paired: (Cv hi|lo of the low nibble, Cv hi|lo of the high nibble) per code byte, entry e
     // of copy c at byte 256 e + 8 c from the table base
     uint2 vtab2[PV ? 256 : 1][PV ? VCOPIES : 1];
     uint32_t vtab[1 << VB];             // Cv hi|lo per value code (generic layout)
     uint32_t wt[NW][16][WTS];           // per-wave transpose of the softmax weights
-    uint32_t limb[4][NH][4][8];         // QJL A operand: limb l of head h, [g][shift] -> 4 bytes (dims 32g + s + 8e)
     union {
         struct {
-            float q[NH][D];
-            float qr[NH][D];            // q R_k^T
-            float qp[NH][D];            // q S^T
-            double sqd[2 * NH];         // sum of int(q_proj * 2^F) over each half (64 dims) of a head
+            uint4 img[IMG_DW / 4];      // this group's q-side image
             uint32_t ksrc[16];          // Ck hi|lo per key code
-            float red[NW];
         } pro;
         struct {
             float o[NW][NH][D];
             float m[NW][NH];
             float s[NW][NH];
         } epi;
+
     } u;
 };
+
+// ----------------------------------------------------------------- merge
+// One query head bh, MT threads (t = 0..MT-1): merge the split partials (maxima in the log2
+// domain), normalise, un-rotate by R_v.  Thread t reads R_v rows k in [16 (t / 32), 16 (t / 32)
+// + 16), columns 4 (t % 32) .. + 3, as float4.  Every thread of the workgroup calls this the
+// same number of times (barriers inside); act = false threads only take part in the barriers.
+__device__ __forceinline__ void merge_head(int bh, bool act, int t, int n_split, const float* __restrict__ part_o,
+                                           const float* __restrict__ part_ml, const float* __restrict__ Rv,
+                                           float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
+                                           float* __restrict__ lse_out, float* so, float4 (*part)[D / 4],
+                                           float (*red)[2]) {
+    const int lane = t & 63, wv = t >> 6;
+    const float* ml = part_ml + (size_t)bh * n_split * 2;
+    float M = NEG_INF;
+    if (act)
+        for (int k = t; k < n_split; k += MT) M = fmaxf(M, ml[2 * k]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) red[wv][0] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
+    // normalised rotated output: threads (half, d) split the splits in two
+    const int d = t & (D - 1), hf = t >> 7;
+    float o = 0.0f, sacc = 0.0f;
+    if (act && M != NEG_INF) {
+        for (int k = hf; k < n_split; k += 2) {
+            const float mk = ml[2 * k];
+            const float e = mk == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
+            o = __builtin_fmaf(e, part_o[((size_t)bh * n_split + k) * D + d], o);
+            sacc = __builtin_fmaf(e, ml[2 * k + 1], sacc);
+        }
+    }
+    float* po2 = reinterpret_cast<float*>(part);
+    po2[t] = o;
+    if (d == 0) red[hf][1] = sacc;
+    __syncthreads();
+    if (t < D) {
+        const float sum = red[0][1] + red[1][1];
+        so[t] = (M != NEG_INF) ? (po2[t] + po2[t + D]) / fmaxf(sum, 1e-8f) : 0.0f;
+        if (act && lse_out && t == 0) lse_out[bh] = (M != NEG_INF) ? M * LN2 + logf(sum) : NEG_INF;
+    }
+    __syncthreads();
+    const int c4 = t & 31, kr = t >> 5;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4* rv4 = reinterpret_cast<const float4*>(Rv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = 16 * kr + i;
+        const float4 r = rv4[(size_t)k * (D / 4) + c4];
+        const float w = so[k];
+        acc.x = __builtin_fmaf(w, r.x, acc.x);
+        acc.y = __builtin_fmaf(w, r.y, acc.y);
+        acc.z = __builtin_fmaf(w, r.z, acc.z);
+        acc.w = __builtin_fmaf(w, r.w, acc.w);
+    }
+    __syncthreads();  // so / po2 reads above are done before part is overwritten
+    part[kr][c4] = acc;
+    __syncthreads();
+    if (act && t < D) {
+        const float* pf = reinterpret_cast<const float*>(part);
+        float a = 0.0f;
+#pragma unroll
+        for (int r = 0; r < MT / 32; ++r) a += pf[r * D + t];
+        if (out_f32) out_f32[(size_t)bh * D + t] = a;
+        if (out_bf16) out_bf16[(size_t)bh * D + t] = (uint16_t)tq::f32_to_bf16(a);
+    }
+    __syncthreads();  // scratch reused by the next head
+}
+
+// One workgroup per (batch row, query head).
+__global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                                                   int n_split, const float* __restrict__ Rv,
+                                                   float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
+                                                   float* __restrict__ lse_out) {
+    __shared__ float so[D];
+    __shared__ float4 part[MT / 32][D / 4];
+    __shared__ float red[MT / 64][2];
+    merge_head(blockIdx.x, true, threadIdx.x, n_split, part_o, part_ml, Rv, out_f32, out_bf16, lse_out, so, part, red);
+}
+
+// ------------------------------------------------------------------ prep kernel
+// One workgroup per (batch row, KV head): q_rot = q R_k^T and q_proj = q S^T for the group's
+// query heads (reference runtime/triton_kernels.py:289, 305-306), split into the MFMA
+// operand layouts the split kernel holds in registers:
+//   key score: lane (n, g), MFMA j, VGPR r = q_x[h][32 g + 4 j + r] twice (bf16), row n =
+//              R::row(h, x), x = 0: bf16(q_rot), x = 1: bf16(q_rot - bf16(q_rot));
+//   QJL:       x = rint(q_proj 2^F) with |x| < 2^30 in balanced base-256 digits (int8 limbs),
+//              rows (head, limb), byte e of VGPR v of MFMA jj <-> dim 32 g + 4 jj + v + 8 e;
+//              sum_d x per head (exact) and 2^(1-F) for the sign-bit identity.
+constexpr int PT = 512;  // prep threads: (matrix, output dim, half of the dot product)
+template <bool QJL, int GC>
+__global__ __launch_bounds__(PT) void prep_kernel(const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G,
+                                                  const float* __restrict__ Rk, const float* __restrict__ S,
+                                                  uint32_t* __restrict__ img) {
+    using R = Rows<GC>;
+    constexpr int NH = R::NH;
+    constexpr int NWP = PT / 64;
+    __shared__ float qs[NH][D];
+    __shared__ float qr[NH][D];
+    __shared__ float qp[NH][D];
+    __shared__ double sqd[2 * NH];
+    __shared__ float red[NWP];
+    __shared__ uint32_t limb[4][NH][4][8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = blockIdx.x;
+    const int b = grp / kv_heads, kvh = grp - b * kv_heads;
+    const int bh0 = b * q_heads + kvh * G;
+    uint32_t* out = img + (size_t)grp * IMG_DW;
+
+    for (int i = tid; i < NH * D; i += PT) {
+        const int h = i / D, d = i % D;
+        qs[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
+    }
+    constexpr int MATS = QJL ? 2 : 1;
+    const bool mv_thread = tid < MATS * 2 * D;
+    const int hf = tid & 1, j = (tid >> 1) & (D - 1), mat = tid >> 8;
+    float4 r4[16];
+    if (mv_thread) {
+        const float4* row = reinterpret_cast<const float4*>((mat ? S : Rk) + (size_t)j * D) + 16 * hf;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r4[i] = row[i];
+    }
+    __syncthreads();
+    if (mv_thread) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const float4* qh = reinterpret_cast<const float4*>(qs[h]) + 16 * hf;
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float4 x = qh[i];
+                a = __builtin_fmaf(x.x, r4[i].x, a);
+                a = __builtin_fmaf(x.y, r4[i].y, a);
+                a = __builtin_fmaf(x.z, r4[i].z, a);
+                a = __builtin_fmaf(x.w, r4[i].w, a);
+            }
+            a += __shfl_xor(a, 1);
+            if (hf == 0) (mat ? qp : qr)[h][j] = a;
+        }
+    }
+    __syncthreads();
+
+    int F = 0;
+    if constexpr (QJL) {
+        float mx = 0.0f;
+        for (int i = tid; i < NH * D; i += PT) mx = fmaxf(mx, fabsf((&qp[0][0])[i]));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        mx = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWP; ++w) mx = fmaxf(mx, red[w]);
+        int e = 0;
+        if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
+        F = 30 - e;
+        F = F > 100 ? 100 : F;
+        const float sc = ldexpf(1.0f, F);
+        // thread -> (head h, dim d); a wave covers 64 dims of one head, whose sum of x is
+        // exact in fp64 (|x| < 2^30)
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&limb[0][0][0][0]);
+        for (int i = tid; i < NH * D; i += PT) {
+            const int h = i / D, d = i % D;
+            int x = (int)rintf(qp[h][d] * sc);
+            double xs = (double)x;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) xs += __shfl_xor(xs, off);
+            if (lane == 0) sqd[i >> 6] = xs;
+            const int gg = d >> 5, sh = d & 7, e8 = (d >> 3) & 3;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int l = ((x + 128) & 255) - 128;
+                lb[(((k * NH + h) * 4 + gg) * 8 + sh) * 4 + e8] = (uint8_t)(l & 255);
+                x = (x - l) >> 8;
+            }
+        }
+        __syncthreads();
+    }
+
+    // key-score A operand image: dword (j, lane, r)
+    for (int i = tid; i < 8 * 64 * 4; i += PT) {
+        const int jj = i >> 8, ln = (i >> 2) & 63, r = i & 3;
+        const int n = ln & 15, g = ln >> 4;
+        const int h_row = GC == 1 ? n / 4 : n / 2;
+        const int x_row = GC == 1 ? n % 4 : n % 2;
+        uint32_t v = 0;
+        if (x_row < 2 && h_row < G) {
+            const float x = qr[h_row][32 * g + 4 * jj + r];
+            const float hi = bf16_val(bf16_bits(x));
+            v = dup_bf16(x_row == 0 ? hi : x - hi);
+        }
+        out[IMG_QA + i] = v;
+    }
+    if constexpr (QJL) {
+        for (int i = tid; i < R::NQJ * 2 * 64 * 4; i += PT) {
+            const int set = i >> 9, jj = (i >> 8) & 1, ln = (i >> 2) & 63, v = i & 3;
+            const int n = ln & 15, g = ln >> 4;
+            const int h = GC == 1 ? n / 4 : n / 2;
+            const int l = GC == 1 ? n % 4 : 2 * set + (n % 2);
+            out[IMG_QJ + i] = limb[l][h][g][4 * jj + v];
+        }
+        if (tid < NH) {
+            const float sqv = (float)((sqd[2 * tid] + sqd[2 * tid + 1]) * (double)ldexpf(1.0f, -F));
+            out[IMG_SQ + tid] = __float_as_uint(sqv);
+        }
+        if (tid == 0) out[IMG_QFIX] = __float_as_uint(ldexpf(1.0f, 1 - F));
+    }
+}
 
 template <int KB, int VB, bool QJL, int GC>
 __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
-    const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vn, const float* __restrict__ Rk,
-    const float* __restrict__ Ck, const float* __restrict__ S, const float* __restrict__ Cv, float scale,
+    const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vn, const uint32_t* __restrict__ qimg,
+    const float* __restrict__ Ck, const float* __restrict__ Cv, float scale,
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
     using Sm = Smem<KB, VB, QJL, GC>;
     using R = Rows<GC>;
@@ -357,142 +580,50 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     };
 
     // ------------------------------------------------------------ prologue
-    // round 1: every global read of the prologue is issued before the first barrier (one
-    // memory round trip): codebooks (hi|lo), q, and the R_k / S rows of the mat-vec threads
+    // round 1: codebooks (hi|lo) and the group's q-side image from prep_kernel (one 16-byte
+    // read per thread; every split workgroup of the group reads the same L2-resident bytes)
     if (tid < (1 << KB)) sm.u.pro.ksrc[tid] = pack_hilo(Ck[tid]);
     if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = pack_hilo(Cv[tid - 64]);
-    for (int i = tid; i < NH * D; i += NT) {
-        const int h = i / D, d = i % D;
-        sm.u.pro.q[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(qimg + (size_t)grp * IMG_DW);
+        for (int i = tid; i < IMG_DW / 4; i += NT) sm.u.pro.img[i] = src[i];
     }
     // zero slots of the weight transpose (never written by the loop)
     for (int i = tid; i < NW * 16 * Sm::WTS; i += NT) (&sm.wt[0][0][0])[i] = 0u;
-    // q_rot[h][j] = q[h] . R_k[j], q_proj[h][j] = q[h] . S[j]: thread -> (matrix, dim j,
-    // half of the dot product), 16 independent float4 loads; halves joined by a shuffle
-    constexpr int MATS = QJL ? 2 : 1;
-    const bool mv_thread = tid < MATS * 2 * D;
-    const int mv_hf = tid & 1, mv_j = (tid >> 1) & (D - 1), mv_mat = tid >> 8;
-    float4 r4[16];
-    if (mv_thread) {
-        const float4* row = reinterpret_cast<const float4*>((mv_mat ? S : Rk) + (size_t)mv_j * D) + 16 * mv_hf;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) r4[i] = row[i];
-    }
     __syncthreads();
-    // round 2 (LDS only): pair tables expanded from the codebooks, then the mat-vecs
-    for (int i = tid; i < (1 << (2 * KB)); i += NT)
-        sm.ktab[i] = make_uint2(sm.u.pro.ksrc[i & ((1 << KB) - 1)], sm.u.pro.ksrc[i >> KB]);
+    // round 2 (LDS only): pair tables expanded from the codebooks; operands into registers
+    for (int i = tid; i < (1 << (2 * KB)) * Sm::KC; i += NT) {
+        const int e = i / Sm::KC;
+        (&sm.ktab[0][0])[i] = make_uint2(sm.u.pro.ksrc[e & ((1 << KB) - 1)], sm.u.pro.ksrc[e >> KB]);
+    }
     if constexpr (Sm::PV) {
         for (int i = tid; i < 256 * VCOPIES; i += NT) {
             const int e = i / VCOPIES;
             (&sm.vtab2[0][0])[i] = make_uint2(sm.vtab[e & 15], sm.vtab[e >> 4]);
         }
     }
-    {
-        if (mv_thread) {
-            const int hf = mv_hf, j = mv_j, mat = mv_mat;
-            float acc[NH];
-#pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                const float4* qh = reinterpret_cast<const float4*>(sm.u.pro.q[h]) + 16 * hf;
-                float a = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float4 x = qh[i];
-                    a = __builtin_fmaf(x.x, r4[i].x, a);
-                    a = __builtin_fmaf(x.y, r4[i].y, a);
-                    a = __builtin_fmaf(x.z, r4[i].z, a);
-                    a = __builtin_fmaf(x.w, r4[i].w, a);
-                }
-                acc[h] = a + __shfl_xor(a, 1);
-            }
-            if (hf == 0) {
-#pragma unroll
-                for (int h = 0; h < NH; ++h) (mat ? sm.u.pro.qp : sm.u.pro.qr)[h][j] = acc[h];
-            }
-        }
-    }
-    __syncthreads();
-
-    // fixed-point scale of q_proj: |q_proj * 2^F| < 2^30, so four balanced int8 limbs hold it
-    int F = 0;
-    if constexpr (QJL) {
-        float mx = 0.0f;
-        for (int i = tid; i < NH * D; i += NT) mx = fmaxf(mx, fabsf((&sm.u.pro.qp[0][0])[i]));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        if (lane == 0) sm.u.pro.red[wave] = mx;
-        __syncthreads();
-        mx = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm.u.pro.red[w]);
-        int e = 0;
-        if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
-        F = 30 - e;
-        F = F > 100 ? 100 : F;
-        const float sc = ldexpf(1.0f, F);
-        // thread -> (head h, dim d): balanced base-256 digits of x = rint(q_proj 2^F),
-        // x = l0 + 2^8 l1 + 2^16 l2 + 2^24 l3, l_i in [-128, 127]; byte layout per lane
-        // group g and shift s: dims 32 g + s + 8 e, e = 0..3
-        // sum_d x per head: 64 consecutive elements (one wave, one head) summed exactly in
-        // fp64 (|x| < 2^30, 64 terms), the NH * D / 64 wave sums combined after the barrier
-        uint8_t* lb = reinterpret_cast<uint8_t*>(&sm.limb[0][0][0][0]);
-        for (int i = tid; i < NH * D; i += NT) {
-            const int h = i / D, d = i % D;
-            int x = (int)rintf(sm.u.pro.qp[h][d] * sc);
-            double xs = (double)x;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) xs += __shfl_xor(xs, off);
-            if (lane == 0) sm.u.pro.sqd[i >> 6] = xs;
-            const int gg = d >> 5, s = d & 7, e = (d >> 3) & 3;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int l = ((x + 128) & 255) - 128;
-                lb[(((k * NH + h) * 4 + gg) * 8 + s) * 4 + e] = (uint8_t)(l & 255);
-                x = (x - l) >> 8;
-            }
-        }
-        __syncthreads();
-    }
-
-    // A operands of the key-score MFMAs (32 VGPRs): lane (i = n, g), MFMA j, VGPR r holds
+    const uint32_t* im = reinterpret_cast<const uint32_t*>(sm.u.pro.img);
+    // A operands of the key-score MFMAs (32 VGPRs): lane (n, g), MFMA j, VGPR r holds
     // q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo codebook parts).
-    const int h_row = GC == 1 ? n / 4 : n / 2;
-    const int x_row = GC == 1 ? n % 4 : n % 2;
-    const bool row_live = x_row < 2 && h_row < G;
     u32x4 qa[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            uint32_t v = 0;
-            if (row_live) {
-                const float x = sm.u.pro.qr[h_row][32 * g + 4 * j + r];
-                const float hi = bf16_val(bf16_bits(x));
-                v = dup_bf16(x_row == 0 ? hi : x - hi);
-            }
-            qa[j][r] = v;
-        }
+    for (int j = 0; j < 8; ++j) qa[j] = *reinterpret_cast<const u32x4*>(im + IMG_QA + (j * 64 + lane) * 4);
     // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
     // 32 g + 4 jj + v + 8 e.
     u32x4 qj[R::NQJ][2];
     float sq[R::HPL];
+    float qfix = 0.0f;  // sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp, in units of 2^-F
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) sq[i] = 0.0f;
     if constexpr (QJL) {
 #pragma unroll
-        for (int set = 0; set < R::NQJ; ++set) {
-            const int h = GC == 1 ? n / 4 : n / 2;
-            const int limb = GC == 1 ? n % 4 : 2 * set + (n % 2);
+        for (int set = 0; set < R::NQJ; ++set)
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
+                qj[set][jj] = *reinterpret_cast<const u32x4*>(im + IMG_QJ + ((set * 2 + jj) * 64 + lane) * 4);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) qj[set][jj][v] = sm.limb[limb][h][g][4 * jj + v];
-        }
-#pragma unroll
-        for (int i = 0; i < R::HPL; ++i)
-            sq[i] = (float)((sm.u.pro.sqd[2 * (R::HPL * g + i)] + sm.u.pro.sqd[2 * (R::HPL * g + i) + 1]) *
-                            (double)ldexpf(1.0f, -F));
+        for (int i = 0; i < R::HPL; ++i) sq[i] = __uint_as_float(im[IMG_SQ + R::HPL * g + i]);
+        qfix = __uint_as_float(im[IMG_QFIX]);
     }
     __syncthreads();  // the prologue area is reused by the epilogue
 
@@ -508,7 +639,6 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
 
     const float c_mse = scale * LOG2E;
     const float c_qjl = scale * LOG2E * QJL_SCALE;
-    const float qfix = ldexpf(1.0f, 1 - F);  // sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp
     uint32_t(*wt)[Sm::WTS] = sm.wt[wave];
     // generic layout: token 4 r + g sits at k-slot pair 4 g + r
     const int wslot = 4 * (n & 3) + (n >> 2);
@@ -516,21 +646,27 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     // two tokens) -> dwords 4 (4 u + k) + 2 s + p of rows (head, p, x)
     const int pslot = 4 * (4 * (n >> 3) + (n & 3)) + 2 * ((n >> 2) & 1);
     const uint32_t plane = 8u * (uint32_t)(lane & (VCOPIES - 1));  // copy of the pair table
+    constexpr int KSHIFT = Sm::KC == 32 ? 8 : (Sm::KC == 8 ? 6 : 3);  // log2 bytes per key-table entry row
+    const uint32_t klane = 8u * (uint32_t)(lane & (Sm::KC - 1));
 
     auto process = [&](const Blk& B, int64_t tb) {
         // ---- key scores: 8 MFMAs over dims 32 g + 4 j + r
-        f32x4 acc_k = f32x4{0.f, 0.f, 0.f, 0.f};
+        // two independent accumulation chains (even / odd j) halve the dependent MFMA latency
+        f32x4 acc_k = f32x4{0.f, 0.f, 0.f, 0.f}, acc_k1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             u32x4 bk;
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                const uint32_t off = field_x<2 * KB, 3>(B.kw, (4 * j + 2 * p) * KB);
+                const uint32_t off = field_x<2 * KB, KSHIFT>(B.kw, (4 * j + 2 * p) * KB) | klane;
                 const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.ktab) + off);
                 bk[2 * p] = e.x;
                 bk[2 * p + 1] = e.y;
             }
-            acc_k = mfma_bf16(qa[j], bk, acc_k);
+            if (j & 1)
+                acc_k1 = mfma_bf16(qa[j], bk, acc_k1);
+            else
+                acc_k = mfma_bf16(qa[j], bk, acc_k);
         }
         // ---- QJL sums
         i32x4 acc_q[R::NQJ];
@@ -555,7 +691,7 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         bool over = false;
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i) {
-            float v = knf * (acc_k[2 * i] + acc_k[2 * i + 1]);
+            float v = knf * ((acc_k[2 * i] + acc_k1[2 * i]) + (acc_k[2 * i + 1] + acc_k1[2 * i + 1]));
             if constexpr (QJL) {
                 float qs;
                 if constexpr (GC == 1) {
@@ -755,73 +891,6 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     }
 }
 
-// ----------------------------------------------------------------- merge
-// One workgroup per (batch row, query head): merge the split partials (maxima in
-// the log2 domain), normalise, un-rotate by R_v.  Thread t reads R_v rows
-// k in [16 (t / 32), 16 (t / 32) + 16), columns 4 (t % 32) .. + 3, as float4.
-constexpr int MT = 256;
-__global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
-                                                   int n_split, const float* __restrict__ Rv,
-                                                   float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
-                                                   float* __restrict__ lse_out) {
-    __shared__ float so[D];
-    __shared__ float4 part[MT / 32][D / 4];
-    __shared__ float red[MT / 64][2];
-    const int bh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const float* ml = part_ml + (size_t)bh * n_split * 2;
-    float M = NEG_INF;
-    for (int k = tid; k < n_split; k += MT) M = fmaxf(M, ml[2 * k]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (lane == 0) red[wv][0] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
-    // normalised rotated output: threads (half, d) split the splits in two
-    const int d = tid & (D - 1), hf = tid >> 7;
-    float o = 0.0f, s = 0.0f;
-    if (M != NEG_INF) {
-        for (int k = hf; k < n_split; k += 2) {
-            const float mk = ml[2 * k];
-            const float e = mk == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
-            o = __builtin_fmaf(e, part_o[((size_t)bh * n_split + k) * D + d], o);
-            s = __builtin_fmaf(e, ml[2 * k + 1], s);
-        }
-    }
-    float* po2 = reinterpret_cast<float*>(part);
-    po2[tid] = o;
-    if (d == 0) red[hf][1] = s;
-    __syncthreads();
-    if (tid < D) {
-        const float sum = red[0][1] + red[1][1];
-        so[tid] = (M != NEG_INF) ? (po2[tid] + po2[tid + D]) / fmaxf(sum, 1e-8f) : 0.0f;
-        if (lse_out && tid == 0) lse_out[bh] = (M != NEG_INF) ? M * LN2 + logf(sum) : NEG_INF;
-    }
-    __syncthreads();
-    const int c4 = tid & 31, kr = tid >> 5;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4* rv4 = reinterpret_cast<const float4*>(Rv);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int k = 16 * kr + i;
-        const float4 r = rv4[(size_t)k * (D / 4) + c4];
-        const float w = so[k];
-        acc.x = __builtin_fmaf(w, r.x, acc.x);
-        acc.y = __builtin_fmaf(w, r.y, acc.y);
-        acc.z = __builtin_fmaf(w, r.z, acc.z);
-        acc.w = __builtin_fmaf(w, r.w, acc.w);
-    }
-    part[kr][c4] = acc;
-    __syncthreads();
-    if (tid < D) {
-        const float* pf = reinterpret_cast<const float*>(part);
-        float a = 0.0f;
-#pragma unroll
-        for (int r = 0; r < MT / 32; ++r) a += pf[r * D + tid];
-        if (out_f32) out_f32[(size_t)bh * D + tid] = a;
-        if (out_bf16) out_bf16[(size_t)bh * D + tid] = (uint16_t)tq::f32_to_bf16(a);
-    }
-}
-
 struct SplitArgs {
     const uint16_t* q;
     int q_heads, kv_heads, G;
@@ -833,7 +902,8 @@ struct SplitArgs {
     const uint16_t* kr;
     const uint8_t* vc;
     const uint16_t* vn;
-    const float *Rk, *Ck, *S, *Cv;
+    const uint32_t* qimg;
+    const float *Ck, *Cv;
     float scale;
     int64_t tps;
     int n_split;
@@ -892,7 +962,7 @@ int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out
     if (a.po == nullptr) return TQ_OK;  // sizing query only
     hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC>::NT), 0, s, a.q, a.q_heads,
                        a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
-                       a.vn, a.Rk, a.Ck, a.S, a.Cv, a.scale, tps, ns, a.po, a.pml);
+                       a.vn, a.qimg, a.Ck, a.Cv, a.scale, tps, ns, a.po, a.pml);
     return TQ_OK;
 }
 
@@ -963,7 +1033,7 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int groups = batch * kv_heads;
     SplitArgs a{q, q_heads, kv_heads, G, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms,
-                v_codes, v_norms, key_rotation, key_centers, qjl, value_centers, scale, 0, 0, nullptr, nullptr};
+                v_codes, v_norms, nullptr, key_centers, value_centers, scale, 0, 0, nullptr, nullptr};
     int n_split = 0;
     int64_t tps = 0;
     int st = dispatch(value_bits, has_qjl, G, a, groups, s, &n_split, &tps);  // sizing
@@ -973,6 +1043,25 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     char* base = static_cast<char*>(workspace);
     a.po = reinterpret_cast<float*>(base + w.po);
     a.pml = reinterpret_cast<float*>(base + w.pml);
+    uint32_t* qimg = reinterpret_cast<uint32_t*>(base + w.img);
+    a.qimg = qimg;
+    // q-side operands once per group, then the split pass, then the merge
+    if (G <= 4) {
+        if (has_qjl)
+            hipLaunchKernelGGL((prep_kernel<true, 1>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
+                               key_rotation, qjl, qimg);
+        else
+            hipLaunchKernelGGL((prep_kernel<false, 1>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
+                               key_rotation, qjl, qimg);
+    } else {
+        if (has_qjl)
+            hipLaunchKernelGGL((prep_kernel<true, 2>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
+                               key_rotation, qjl, qimg);
+        else
+            hipLaunchKernelGGL((prep_kernel<false, 2>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
+                               key_rotation, qjl, qimg);
+    }
+    TQ_CHECK_LAUNCH();
     st = dispatch(value_bits, has_qjl, G, a, groups, s, &n_split, &tps);
     if (st != TQ_OK) return st;
     TQ_CHECK_LAUNCH();
