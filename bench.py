@@ -45,6 +45,21 @@ def packed_bytes_per_token_head(dim: int, bits: int, qjl: bool) -> int:
     return b
 
 
+def measured_traffic() -> int | None:
+    """HBM bytes per call from the committed PMC summary, if it was measured on this kernel source."""
+    import hashlib
+
+    summary = ROOT / "profiles" / "tq_decode_attention_c2_traffic.txt"
+    source = ROOT / "tq-local_amd" / "csrc" / "tq_attention.hip"
+    try:
+        fields = dict(line.split(":", 1) for line in summary.read_text().splitlines() if ":" in line and not line.startswith("#"))
+        if fields["attention_source_sha256"].strip() != hashlib.sha256(source.read_bytes()).hexdigest():
+            return None  # stale: the kernel changed since the counters were taken
+        return int(fields["traffic_bytes_per_call"].strip())
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(bits: int = 4) -> dict:
     """BASELINE config 1 (B=1, Hq=32, Hkv=8, N=4096) through the torch restatement of
     the reference's CPU path: encode (K Q_prod + V Q_mse) and one decode-attention step."""
@@ -263,6 +278,8 @@ def main() -> int:
     q_bytes = n_vec * (4 * D + per_tok)
     q_flops = n_vec * 2 * D * D * (4 if qjl else 2)
 
+    is_c2 = (B, Hq, Hkv, N, bits, qjl) == (8, 32, 8, 32768, 4, True)
+    traffic = measured_traffic() if is_c2 else None
     line = {
         "metric": "fused decode-attn us/layer + packed-KV GB/s (% HBM peak), 8B KV shape @32K",
         "value": round(value, 2),
@@ -296,7 +313,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": ("tq_decode_attention = split_kernel + merge_kernel; duration = HIP events around the "
                        "timed graph replays on the launch stream / (steps x layers)"),
             "us_per_call": round(avg_us, 3),
