@@ -74,9 +74,6 @@ constexpr float LN2 = 0.6931471805599453f;
 constexpr float QJL_SCALE = 1.2533141373155003f / D;  // sqrt(pi/2) / D
 constexpr float LAZY_MAX = 8.0f;                      // log2 headroom before the reference max is raised
 constexpr int BUF_DW3 = 0x00020000;                   // buffer descriptor word 3 (gfx9: 32-bit untyped)
-#ifndef TQ_WT_FENCE
-#define TQ_WT_FENCE 1
-#endif
 #ifndef TQ_KV_NT
 #define TQ_KV_NT 2
 #endif
@@ -741,7 +738,9 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
             wq[i][0] = hh;
             wq[i][1] = dup_bf16(w - __uint_as_float(hh & 0xFFFF0000u));
         }
-        // ---- weights -> A operand of the value MFMAs (transpose through LDS)
+        // ---- weights -> A operand of the value MFMAs (transpose through this wave's LDS rows;
+        // one wave's LDS accesses execute in order and the compiler keeps the may-alias
+        // writes and reads of wt in program order, so no fence is needed)
         if constexpr (PV) {
             // rows 4 h + 2 p + x: this lane's head is g; the zero slots are never written
             wt[4 * g + 0][pslot] = wq[0][0];
@@ -756,11 +755,6 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
                 wt[R::row(h, 1)][wslot] = wq[i][1];
             }
         }
-#if TQ_WT_FENCE
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#endif
         if constexpr (PV) {
             // ---- value MFMAs, paired: lane (c = n, k = g) supplies tokens 8 u + 4 s + g, pair
             // column c of group m = code byte m of dword c (dims 8 c + 2 m, 8 c + 2 m + 1)
@@ -821,11 +815,6 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
             vmfma(std::integral_constant<int, 6>{});
             vmfma(std::integral_constant<int, 7>{});
         }
-#if TQ_WT_FENCE
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#endif
     };
 
     if (t0 + (int64_t)wave * BLK < t1) {
