@@ -21,9 +21,10 @@
 //                 codes returning (Ck_hi, Ck_lo) for both.  Every cross product of the
 //                 two-term splits is formed, so the score carries ~2^-17 relative error
 //                 against fp32 inputs (the tolerance is 2e-3 of |out|).
-//   QJL term      v_mfma_i32_16x16x64_i8 on the raw sign bits (bytes of 0/1, two VALU
-//                 ops per 4 dims) against q_proj = q S^T in 32-bit fixed point split in
-//                 four int8 limbs (rows = (head, limb)); exact integer accumulation.
+//   QJL term      v_mfma_i32_16x16x64_i8 on the sign bits left in place (one v_and per 4
+//                 dims: bit i of each byte is worth 2^i, -128 for i = 7) against q_proj =
+//                 q S^T in fixed point divided by the same 2^i, split in four int8 limbs
+//                 (rows = (head, limb)); exact integer accumulation.
 //   softmax       online, base 2 (scores are pre-multiplied by log2 e), with a lazily
 //                 raised reference maximum: weights are exp2(score - m_ref) and m_ref
 //                 is raised (with a rescale of the partial sums) only when a score
@@ -226,6 +227,18 @@ constexpr bool PAIRED = GC == 1 && VB == 4;
 constexpr int VCOPIES = 32;      // lane-private copies of the 256-entry pair table (bank pair per lane)
 constexpr int WT_STRIDE_P = 36;  // dwords per weight row in the paired layout (32 slots + bank spread)
 
+// LDS scratch of the image builder
+template <int GC>
+struct PrepLds {
+    static constexpr int NH = 4 * GC;
+    float qs[NH][D];
+    float qr[NH][D];
+    float qp[NH][D];
+    double sqd[2 * NH];
+    float red[16];
+    uint32_t limb[4][NH][4][8];
+};
+
 template <int KB, int VB, bool QJL, int GC>
 struct Smem {
     static constexpr int NH = 4 * GC;
@@ -341,37 +354,65 @@ __global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ par
 // operand layouts the split kernel holds in registers:
 //   key score: lane (n, g), MFMA j, VGPR r = q_x[h][32 g + 4 j + r] twice (bf16), row n =
 //              R::row(h, x), x = 0: bf16(q_rot), x = 1: bf16(q_rot - bf16(q_rot));
-//   QJL:       x = rint(q_proj 2^F) with |x| < 2^22 in balanced base-256 digits (int8 limbs,
-//              the fourth always zero), rows (head, limb), byte e of VGPR v of MFMA jj <-> dim
-//              32 g + 4 jj + v + 8 e; sum_d x per head (exact) and 2^(1-F), both times the
-//              QJL logit scale.  The key-score operand carries the logit scale times log2 e.
+//   QJL:       x_d = rint(q_proj_d 2^(G2 - d % 8)) (negated for d % 8 = 7) in four balanced
+//              base-256 digits (int8 limbs), rows (head, limb), byte e of VGPR v of MFMA jj <->
+//              dim 32 g + 4 jj + v + 8 e; sum_d y_d (y_d = x_d 2^(d % 8), exact) per head and
+//              2^(1 - G2), both times the QJL logit scale.  The key-score operand carries the
+//              logit scale times log2 e.
 constexpr int PT = 512;  // prep threads: (matrix, output dim, half of the dot product)
-template <bool QJL, int GC>
-__global__ __launch_bounds__(PT) void prep_kernel(const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G,
-                                                  const float* __restrict__ Rk, const float* __restrict__ S,
-                                                  float c_mse, float c_qjl, uint32_t* __restrict__ img) {
+
+// Balanced base-256 digits of x (|x| < 2^29) into the limb image lb[limb][head][d / 32][d % 8]
+// byte (d / 8) % 4.
+template <int NH>
+__device__ __forceinline__ void put_limbs(uint8_t* lb, int h, int d, int x) {
+    const int gg = d >> 5, sh = d & 7, e8 = (d >> 3) & 3;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int l = ((x + 128) & 255) - 128;
+        lb[(((k * NH + h) * 4 + gg) * 8 + sh) * 4 + e8] = (uint8_t)(l & 255);
+        x = (x - l) >> 8;
+    }
+}
+
+// Block-wide max of |v| over NH * D values (v scaled by mul; NTH threads) -> the fixed-point
+// exponent F with max |v| 2^F < 2^22, capped at 60.
+template <int NH, int NTH>
+__device__ __forceinline__ int fixed_exponent(const float* v, float mul, float* red, int tid) {
+    float mx = 0.0f;
+    for (int i = tid; i < NH * D; i += NTH) mx = fmaxf(mx, fabsf(v[i] * mul));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NTH / 64; ++w) mx = fmaxf(mx, red[w]);
+    int e = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
+    const int F = 22 - e;
+    return F > 60 ? 60 : F;
+}
+
+// The q-side image of group grp into out[IMG_DW].  Every thread of the block (NTH >= 512
+// threads) calls it: it holds barriers.
+template <bool QJL, int GC, int NTH>
+__device__ __forceinline__ void build_image(const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, int grp,
+                                            const float* __restrict__ Rk, const float* __restrict__ S, float c_mse,
+                                            float c_qjl, PrepLds<GC>& L, uint32_t* out, int tid) {
+    static_assert(NTH >= 512 && NTH <= 1024 && NTH % 64 == 0, "image builder threads");
     using R = Rows<GC>;
     constexpr int NH = R::NH;
-    constexpr int NWP = PT / 64;
-    __shared__ float qs[NH][D];
-    __shared__ float qr[NH][D];
-    __shared__ float qp[NH][D];
-    __shared__ double sqd[2 * NH];
-    __shared__ float red[NWP];
-    __shared__ uint32_t limb[4][NH][4][8];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int grp = blockIdx.x;
+    const int lane = tid & 63;
     const int b = grp / kv_heads, kvh = grp - b * kv_heads;
     const int bh0 = b * q_heads + kvh * G;
-    uint32_t* out = img + (size_t)grp * IMG_DW;
 
-    for (int i = tid; i < NH * D; i += PT) {
+    for (int i = tid; i < NH * D; i += NTH) {
         const int h = i / D, d = i % D;
-        qs[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
+        L.qs[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
     }
     constexpr int MATS = QJL ? 2 : 1;
     const bool mv_thread = tid < MATS * 2 * D;
-    const int hf = tid & 1, j = (tid >> 1) & (D - 1), mat = tid >> 8;
+    const int hf = tid & 1, j = (tid >> 1) & (D - 1), mat = (tid >> 8) & 1;
     float4 r4[16];
     if (mv_thread) {
         const float4* row = reinterpret_cast<const float4*>((mat ? S : Rk) + (size_t)j * D) + 16 * hf;
@@ -382,7 +423,7 @@ __global__ __launch_bounds__(PT) void prep_kernel(const uint16_t* __restrict__ q
     if (mv_thread) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
-            const float4* qh = reinterpret_cast<const float4*>(qs[h]) + 16 * hf;
+            const float4* qh = reinterpret_cast<const float4*>(L.qs[h]) + 16 * hf;
             float a = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -393,76 +434,70 @@ __global__ __launch_bounds__(PT) void prep_kernel(const uint16_t* __restrict__ q
                 a = __builtin_fmaf(x.w, r4[i].w, a);
             }
             a += __shfl_xor(a, 1);
-            if (hf == 0) (mat ? qp : qr)[h][j] = a;
+            if (hf == 0) (mat ? L.qp : L.qr)[h][j] = a;
         }
     }
     __syncthreads();
 
-    int F = 0;
+    int G2 = 0;  // QJL fixed-point exponent: y_d = q_proj_d 2^G2 (to rounding)
     if constexpr (QJL) {
-        float mx = 0.0f;
-        for (int i = tid; i < NH * D; i += PT) mx = fmaxf(mx, fabsf((&qp[0][0])[i]));
+        // The split kernel feeds sign bit i = d % 8 of every byte in place (byte value 2^i, or
+        // -128 for i = 7), so dim d carries x_d = rint(q_proj_d 2^(G2 - i)) (negated for i = 7)
+        // and contributes y_d = x_d 2^i; |x_d| < 2^29 in four balanced int8 limbs.
+        G2 = fixed_exponent<NH, NTH>(&L.qp[0][0], 1.0f, L.red, tid) + 7;
+        // thread -> (head h, dim d); a wave covers 64 dims of one head, whose sum of y is
+        // exact in fp64
+        uint8_t* lb = reinterpret_cast<uint8_t*>(&L.limb[0][0][0][0]);
+        for (int i = tid; i < NH * D; i += NTH) {
+            const int h = i / D, d = i % D, bit = d & 7;
+            const int x = (int)rintf(L.qp[h][d] * ldexpf(1.0f, G2 - bit));
+            double ys = (double)x * (double)(1 << bit);
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        if (lane == 0) red[wave] = mx;
-        __syncthreads();
-        mx = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NWP; ++w) mx = fmaxf(mx, red[w]);
-        int e = 0;
-        if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
-        F = 22 - e;
-        F = F > 100 ? 100 : F;
-        const float sc = ldexpf(1.0f, F);
-        // thread -> (head h, dim d); a wave covers 64 dims of one head, whose sum of x is
-        // exact in fp64 (|x| < 2^22; the fourth limb is zero)
-        uint8_t* lb = reinterpret_cast<uint8_t*>(&limb[0][0][0][0]);
-        for (int i = tid; i < NH * D; i += PT) {
-            const int h = i / D, d = i % D;
-            int x = (int)rintf(qp[h][d] * sc);
-            double xs = (double)x;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) xs += __shfl_xor(xs, off);
-            if (lane == 0) sqd[i >> 6] = xs;
-            const int gg = d >> 5, sh = d & 7, e8 = (d >> 3) & 3;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int l = ((x + 128) & 255) - 128;
-                lb[(((k * NH + h) * 4 + gg) * 8 + sh) * 4 + e8] = (uint8_t)(l & 255);
-                x = (x - l) >> 8;
-            }
+            for (int off = 32; off > 0; off >>= 1) ys += __shfl_xor(ys, off);
+            if (lane == 0) L.sqd[i >> 6] = ys;
+            put_limbs<NH>(lb, h, d, bit == 7 ? -x : x);
         }
         __syncthreads();
     }
 
     // key-score A operand image: dword (j, lane, r)
-    for (int i = tid; i < 8 * 64 * 4; i += PT) {
+    for (int i = tid; i < 8 * 64 * 4; i += NTH) {
         const int jj = i >> 8, ln = (i >> 2) & 63, r = i & 3;
         const int n = ln & 15, g = ln >> 4;
         const int h_row = GC == 1 ? n / 4 : n / 2;
         const int x_row = GC == 1 ? n % 4 : n % 2;
         uint32_t v = 0;
         if (x_row < 2 && h_row < G) {
-            const float x = qr[h_row][32 * g + 4 * jj + r] * c_mse;  // scores come out in log2 units
+            const float x = L.qr[h_row][32 * g + 4 * jj + r] * c_mse;  // scores come out in log2 units
             const float hi = bf16_val(bf16_bits(x));
             v = dup_bf16(x_row == 0 ? hi : x - hi);
         }
         out[IMG_QA + i] = v;
     }
     if constexpr (QJL) {
-        for (int i = tid; i < R::NQJ * 2 * 64 * 4; i += PT) {
+        for (int i = tid; i < R::NQJ * 2 * 64 * 4; i += NTH) {
             const int set = i >> 9, jj = (i >> 8) & 1, ln = (i >> 2) & 63, v = i & 3;
             const int n = ln & 15, g = ln >> 4;
             const int h = GC == 1 ? n / 4 : n / 2;
             const int l = GC == 1 ? n % 4 : 2 * set + (n % 2);
-            out[IMG_QJ + i] = limb[l][h][g][4 * jj + v];
+            out[IMG_QJ + i] = L.limb[l][h][g][4 * jj + v];
         }
         if (tid < NH) {
-            const float sqv = (float)((sqd[2 * tid] + sqd[2 * tid + 1]) * (double)ldexpf(1.0f, -F) * (double)c_qjl);
+            const float sqv =
+                (float)((L.sqd[2 * tid] + L.sqd[2 * tid + 1]) * (double)ldexpf(1.0f, -G2) * (double)c_qjl);
             out[IMG_SQ + tid] = __float_as_uint(sqv);
         }
-        if (tid == 0) out[IMG_QFIX] = __float_as_uint(ldexpf(1.0f, 1 - F) * c_qjl);
+        if (tid == 0) out[IMG_QFIX] = __float_as_uint(ldexpf(1.0f, 1 - G2) * c_qjl);
     }
+}
+
+template <bool QJL, int GC>
+__global__ __launch_bounds__(PT) void prep_kernel(const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G,
+                                                  const float* __restrict__ Rk, const float* __restrict__ S,
+                                                  float c_mse, float c_qjl, uint32_t* __restrict__ img) {
+    __shared__ PrepLds<GC> L;
+    build_image<QJL, GC, PT>(q, q_heads, kv_heads, G, blockIdx.x, Rk, S, c_mse, c_qjl, L,
+                                 img + (size_t)blockIdx.x * IMG_DW, threadIdx.x);
 }
 
 template <int KB, int VB, bool QJL, int GC>
@@ -675,7 +710,7 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) bq[jj][v] = (B.sw >> (4 * jj + v)) & 0x01010101u;
+                for (int v = 0; v < 4; ++v) bq[jj][v] = B.sw & (0x01010101u << (4 * jj + v));
 #pragma unroll
             for (int set = 0; set < R::NQJ; ++set) {
                 acc_q[set] = mfma_i8(qj[set][0], bq[0], i32x4{0, 0, 0, 0});
@@ -695,13 +730,17 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         for (int i = 0; i < R::HPL; ++i) {
             float v = knf * ((acc_k[2 * i] + acc_k1[2 * i]) + (acc_k[2 * i + 1] + acc_k1[2 * i + 1]));
             if constexpr (QJL) {
-                // sum_d x_d s_d from the three limb sums: |.| < 128 * 2^22, exact in int32
-                int qi;
-                if constexpr (GC == 1)
-                    qi = acc_q[0][0] + (acc_q[0][1] << 8) + (acc_q[0][2] << 16);
-                else
-                    qi = acc_q[0][2 * i] + (acc_q[0][2 * i + 1] << 8) + (acc_q[1][2 * i] << 16);
-                v = __builtin_fmaf(krf, __builtin_fmaf((float)qi, qfix, -sq[i]), v);
+                // sum_d y_d s_d from the four limb sums (each |.| <= 2^21): pairs exact in int32
+                int lo, hi;
+                if constexpr (GC == 1) {
+                    lo = acc_q[0][0] + (acc_q[0][1] << 8);
+                    hi = acc_q[0][2] + (acc_q[0][3] << 8);
+                } else {
+                    lo = acc_q[0][2 * i] + (acc_q[0][2 * i + 1] << 8);
+                    hi = acc_q[1][2 * i] + (acc_q[1][2 * i + 1] << 8);
+                }
+                const float qi = __builtin_fmaf((float)hi, 65536.0f, (float)lo);
+                v = __builtin_fmaf(krf, __builtin_fmaf(qi, qfix, -sq[i]), v);
             }
             lg[i] = valid ? v : NEG_INF;
             over |= lg[i] > m_thr[i];
@@ -1040,22 +1079,18 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     uint32_t* qimg = reinterpret_cast<uint32_t*>(base + w.img);
     a.qimg = qimg;
     // q-side operands once per group, then the split pass, then the merge
-    if (G <= 4) {
-        if (has_qjl)
-            hipLaunchKernelGGL((prep_kernel<true, 1>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
-                               key_rotation, qjl, scale * LOG2E, scale * LOG2E * QJL_SCALE, qimg);
+    {
+        const float c_mse = scale * LOG2E, c_qjl = scale * LOG2E * QJL_SCALE;
+        auto prep = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G, key_rotation, qjl, c_mse,
+                               c_qjl, qimg);
+        };
+        if (G <= 4)
+            has_qjl ? prep(prep_kernel<true, 1>) : prep(prep_kernel<false, 1>);
         else
-            hipLaunchKernelGGL((prep_kernel<false, 1>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
-                               key_rotation, qjl, scale * LOG2E, scale * LOG2E * QJL_SCALE, qimg);
-    } else {
-        if (has_qjl)
-            hipLaunchKernelGGL((prep_kernel<true, 2>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
-                               key_rotation, qjl, scale * LOG2E, scale * LOG2E * QJL_SCALE, qimg);
-        else
-            hipLaunchKernelGGL((prep_kernel<false, 2>), dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G,
-                               key_rotation, qjl, scale * LOG2E, scale * LOG2E * QJL_SCALE, qimg);
+            has_qjl ? prep(prep_kernel<true, 2>) : prep(prep_kernel<false, 2>);
+        TQ_CHECK_LAUNCH();
     }
-    TQ_CHECK_LAUNCH();
     st = dispatch(value_bits, has_qjl, G, a, groups, s, &n_split, &tps);
     if (st != TQ_OK) return st;
     TQ_CHECK_LAUNCH();
