@@ -14,12 +14,12 @@ namespace tq {
 // bf16 bit pattern -> fp32 (exact).
 __device__ __forceinline__ float bf16_to_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
 
-// fp32 -> bf16 bit pattern, round to nearest even (NaN kept quiet).
+// fp32 -> bf16 bit pattern, round to nearest even (NaN kept quiet).  A select rather than a
+// branch: unrolled over a vector, branches would keep every element's value live at once.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-    uint32_t x = __float_as_uint(f);
-    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (x >> 16) | 0x40u;
-    x += 0x7FFFu + ((x >> 16) & 1u);
-    return x >> 16;
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t rounded = (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
+    return ((x & 0x7FFFFFFFu) > 0x7F800000u) ? ((x >> 16) | 0x40u) : rounded;
 }
 
 // fp32 -> IEEE binary16 bit pattern, round to nearest even (v_cvt_f16_f32).

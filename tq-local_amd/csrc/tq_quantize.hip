@@ -59,6 +59,71 @@ struct BitWriter {
     }
 };
 
+// #{i : b[i] < z} (torch.bucketize right=False): one compare and one add-with-carry per
+// boundary; the empty asm keeps the count a plain running sum (no bitmask reassociation).
+template <int NB>
+__device__ __forceinline__ uint32_t bucket_count(float z, const float* __restrict__ b) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        c += (b[i] < z) ? 1u : 0u;
+        __asm__("" : "+v"(c));
+    }
+    return c;
+}
+
+// ---- matrix rows through SGPRs, double-buffered
+// Every multiply-add takes its matrix element from an SGPR (the row is uniform across the
+// wave).  Scalar loads return out of order, so a compiler-placed wait for one chunk also
+// waits for any chunk issued after it; the rows are therefore streamed by hand in CH-float
+// chunks through two SGPR buffers: wait for chunk k, issue chunk k + 1, compute on chunk k.
+// Each wait then covers a load that was issued one chunk of compute earlier.  The kernels
+// using this must not spill SGPRs (a spill copy could read a buffer before its wait).
+typedef float sf16 __attribute__((ext_vector_type(16)));
+template <int CH>
+struct SChunk {
+    sf16 a[CH / 16];
+    __device__ __forceinline__ float operator[](int k) const { return a[k >> 4][k & 15]; }
+};
+__device__ __forceinline__ void sload(SChunk<16>& c, const float* p) {
+    asm volatile("s_load_dwordx16 %0, %1, 0x0" : "=&s"(c.a[0]) : "s"(p) : "memory");
+}
+__device__ __forceinline__ void sload(SChunk<32>& c, const float* p) {
+    asm volatile("s_load_dwordx16 %0, %2, 0x0\n\ts_load_dwordx16 %1, %2, 0x40"
+                 : "=&s"(c.a[0]), "=&s"(c.a[1])
+                 : "s"(p)
+                 : "memory");
+}
+// completes every outstanding scalar load (and LDS access); c is valid afterwards
+__device__ __forceinline__ void swait(SChunk<16>& c) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c.a[0])); }
+__device__ __forceinline__ void swait(SChunk<32>& c) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c.a[0]), "+s"(c.a[1]));
+}
+
+// Streams the D rows of the row-major D x D matrix M (uniform pointer): chunk(d0, C) is
+// called for d0 = 0, CH, 2 CH, ... with C[k] = M[j][d0 + k], then row_end(j).
+template <int CH, typename ChunkFn, typename RowFn>
+__device__ __forceinline__ void stream_rows(const float* M, ChunkFn&& chunk, RowFn&& row_end) {
+    constexpr int NC = D / CH;  // chunks per row (even)
+    SChunk<CH> A, B;
+    sload(A, M);
+    for (int j = 0; j < D; ++j) {
+        const float* mj = M + j * D;
+        const float* next = M + (j + 1 < D ? j + 1 : j) * D;  // the last row reloads itself
+#pragma unroll
+        for (int c = 0; c < NC; c += 2) {
+            swait(A);
+            sload(B, mj + (c + 1) * CH);
+            chunk(c * CH, A);
+            swait(B);
+            sload(A, c + 2 < NC ? mj + (c + 2) * CH : next);
+            chunk((c + 1) * CH, B);
+        }
+        row_end(j);
+    }
+    swait(A);  // no scalar load may still be writing registers the caller reuses
+}
+
 template <int BITS, bool PROD>
 __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
     const uint16_t* __restrict__ x, int heads, int64_t tokens, int64_t n_vec, int64_t x_sb, int64_t x_sh,
@@ -81,29 +146,49 @@ __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
     const int64_t slot = gh * out_cap + out_offset + t;
 
     // ---- load x, norm
+    const uint4* x4 = reinterpret_cast<const uint4*>(xv);
+    auto unpack8 = [](const uint4& w, float* o) {
+        o[0] = tq::bf16_to_f32(w.x & 0xFFFFu);
+        o[1] = tq::bf16_to_f32(w.x >> 16);
+        o[2] = tq::bf16_to_f32(w.y & 0xFFFFu);
+        o[3] = tq::bf16_to_f32(w.y >> 16);
+        o[4] = tq::bf16_to_f32(w.z & 0xFFFFu);
+        o[5] = tq::bf16_to_f32(w.z >> 16);
+        o[6] = tq::bf16_to_f32(w.w & 0xFFFFu);
+        o[7] = tq::bf16_to_f32(w.w >> 16);
+    };
     float u[D];
-    {
-        const uint4* x4 = reinterpret_cast<const uint4*>(xv);
+    float ss = 0.0f;
+    if constexpr (PROD) {
+        // the norm from one streamed pass over x, then x read again into u / n: the raw vector
+        // and u are never live together (keeps the Q_prod kernel at three waves per SIMD)
 #pragma unroll
         for (int i = 0; i < D / 8; ++i) {
-            uint4 w = x4[i];
-            u[8 * i + 0] = tq::bf16_to_f32(w.x & 0xFFFFu);
-            u[8 * i + 1] = tq::bf16_to_f32(w.x >> 16);
-            u[8 * i + 2] = tq::bf16_to_f32(w.y & 0xFFFFu);
-            u[8 * i + 3] = tq::bf16_to_f32(w.y >> 16);
-            u[8 * i + 4] = tq::bf16_to_f32(w.z & 0xFFFFu);
-            u[8 * i + 5] = tq::bf16_to_f32(w.z >> 16);
-            u[8 * i + 6] = tq::bf16_to_f32(w.w & 0xFFFFu);
-            u[8 * i + 7] = tq::bf16_to_f32(w.w >> 16);
-        }
-    }
-    float ss = 0.0f;
+            float e[8];
+            unpack8(x4[i], e);
 #pragma unroll
-    for (int d = 0; d < D; ++d) ss = __builtin_fmaf(u[d], u[d], ss);
+            for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(e[k], e[k], ss);
+        }
+        __asm__ volatile("" ::: "memory");  // a second read, not a copy held from the first
+    } else {
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) unpack8(x4[i], &u[8 * i]);
+#pragma unroll
+        for (int d = 0; d < D; ++d) ss = __builtin_fmaf(u[d], u[d], ss);
+    }
     float n = tq::sqrt_rn(ss);
     if (!(n > 0.0f)) n = 1.0f;
+    if constexpr (PROD) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) u[d] = tq::div_rn(u[d], n);
+        for (int i = 0; i < D / 8; ++i) {
+            unpack8(x4[i], &u[8 * i]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) u[8 * i + k] = tq::div_rn(u[8 * i + k], n);
+        }
+    } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d) u[d] = tq::div_rn(u[d], n);
+    }
     const uint32_t n16 = tq::f32_to_f16(n);
     norms[slot] = (uint16_t)n16;
 
@@ -112,21 +197,35 @@ __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
     constexpr int ROW = D * BITS / 8;
     uint32_t* crow = reinterpret_cast<uint32_t*>(codes + slot * ROW);
     BitWriter bw;
-    for (int j = 0; j < D; ++j) {
-        const float* rj = R + j * D;
-        float z = 0.0f;
+    if constexpr (PROD) {
+        for (int j = 0; j < D; ++j) {
+            const float* rj = R + j * D;
+            float z = 0.0f;
 #pragma unroll
-        for (int d = 0; d < D; ++d) z = __builtin_fmaf(u[d], rj[d], z);
-        uint32_t c = 0;
+            for (int d = 0; d < D; ++d) z = __builtin_fmaf(u[d], rj[d], z);
+            const uint32_t c = bucket_count<NB>(z, boundaries);
+            bw.put(c, BITS, crow);
+            s_code[j][threadIdx.x] = (uint8_t)c;
+        }
+    } else {
+    float z = 0.0f;
+    constexpr int CH = 32;
+    stream_rows<CH>(
+        R,
+        [&](int d0, const SChunk<CH>& C) {
 #pragma unroll
-        for (int i = 0; i < NB; ++i) c += (boundaries[i] < z) ? 1u : 0u;
-        bw.put(c, BITS, crow);
-        if (PROD) s_code[j][threadIdx.x] = (uint8_t)c;
+            for (int k = 0; k < CH; ++k) z = __builtin_fmaf(u[d0 + k], C[k], z);
+        },
+        [&](int j) {
+            const uint32_t c = bucket_count<NB>(z, boundaries);
+            z = 0.0f;
+            bw.put(c, BITS, crow);
+        });
     }
 
     if constexpr (PROD) {
         // ---- residual decode khat = bf16((C[code] @ R) * f32(f16(n))), accumulated row by row
-        float acc[D];
+        float* acc = u;  // u is dead after the rotation: one 128-register array
 #pragma unroll
         for (int d = 0; d < D; ++d) acc[d] = 0.0f;
         for (int j = 0; j < D; ++j) {
@@ -136,7 +235,7 @@ __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
             for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
         }
         const float nf = tq::f16_to_f32(n16);
-        const uint4* x4 = reinterpret_cast<const uint4*>(xv);
+        __asm__ volatile("" ::: "memory");  // x is re-read here, not held across the loop above
         float rs = 0.0f;
 #pragma unroll
         for (int i = 0; i < D / 8; ++i) {
