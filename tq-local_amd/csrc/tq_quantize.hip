@@ -124,6 +124,33 @@ __device__ __forceinline__ void stream_rows(const float* M, ChunkFn&& chunk, Row
     swait(A);  // no scalar load may still be writing registers the caller reuses
 }
 
+// The same count by binary search over the sorted boundaries (the predicate b[i] < z holds on
+// a prefix): BITS compares, and at level l a select tree over the 2^l candidate thresholds
+// driven by the earlier outcomes (2^BITS - BITS - 1 selects in all, against 2^BITS - 1
+// compare/add pairs for the linear count).
+template <int BITS>
+__device__ __forceinline__ uint32_t bucket_search(float z, const float* __restrict__ b) {
+    bool p[BITS];
+    uint32_t c = 0;
+#pragma unroll
+    for (int lvl = 0; lvl < BITS; ++lvl) {
+        const int s = 1 << (BITS - 1 - lvl);
+        float cand[1 << lvl];
+#pragma unroll
+        for (int m = 0; m < (1 << lvl); ++m) cand[m] = b[s - 1 + 2 * s * m];
+        // candidate m = sum_q p[q] 2^(lvl - 1 - q): reduce by the last outcome first
+#pragma unroll
+        for (int q = lvl - 1; q >= 0; --q) {
+            const int half = 1 << q;  // entries left after this step
+#pragma unroll
+            for (int m = 0; m < half; ++m) cand[m] = p[q] ? cand[2 * m + 1] : cand[2 * m];
+        }
+        p[lvl] = cand[0] < z;
+        c |= p[lvl] ? (uint32_t)s : 0u;
+    }
+    return c;
+}
+
 template <int BITS, bool PROD>
 __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
     const uint16_t* __restrict__ x, int heads, int64_t tokens, int64_t n_vec, int64_t x_sb, int64_t x_sh,
@@ -203,7 +230,7 @@ __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
             float z = 0.0f;
 #pragma unroll
             for (int d = 0; d < D; ++d) z = __builtin_fmaf(u[d], rj[d], z);
-            const uint32_t c = bucket_count<NB>(z, boundaries);
+            const uint32_t c = bucket_search<BITS>(z, boundaries);
             bw.put(c, BITS, crow);
             s_code[j][threadIdx.x] = (uint8_t)c;
         }
