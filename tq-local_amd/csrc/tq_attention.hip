@@ -856,23 +856,25 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         }
     };
 
-    if (t0 + (int64_t)wave * BLK < t1) {
+    // blocks of this wave: wave, wave + NW, ... (scalar count)
+    const int64_t first = (int64_t)wave * BLK;
+    const int nb = first < ntok ? (int)((ntok - first + step - 1) / step) : 0;
+    if (nb > 0) {
         // two of this wave's blocks in flight: while one is processed the next-but-one is
         // loaded into the register set just consumed, so A and Bq alternate without copies
         Blk A, Bq;
-        int64_t tb = t0 + (int64_t)wave * BLK;
+        int64_t tb = t0 + first;
         load(A, tb);
-        if (tb + step < t1) load(Bq, tb + step);
-        while (true) {
+        if (nb > 1) load(Bq, tb + step);
+        int i = 0;
+        for (; i + 2 <= nb; i += 2) {
             process(A, tb);
-            tb += step;
-            if (tb >= t1) break;
-            if (tb + step < t1) load(A, tb + step);
-            process(Bq, tb);
-            tb += step;
-            if (tb >= t1) break;
-            if (tb + step < t1) load(Bq, tb + step);
+            if (i + 2 < nb) load(A, tb + 2 * step);
+            process(Bq, tb + step);
+            if (i + 3 < nb) load(Bq, tb + 3 * step);
+            tb += 2 * step;
         }
+        if (i < nb) process(A, tb);
     }
 
     // ------------------------------------------------------------ epilogue
