@@ -3,14 +3,15 @@
 // Two launches per call, on the caller's stream:
 //
 //   split_kernel  grid (n_split, batch * kv_heads), NW waves per workgroup.  A
-//                 workgroup owns a contiguous token range of one (batch row, KV
-//                 head); each wave owns a contiguous sub-range and walks it in
-//                 blocks of 16 tokens.  All G query heads of the GQA group share
-//                 every K/V byte read (reference runtime/triton_kernels.py:84-198
-//                 re-reads the tile once per query head).
-//   merge_kernel  one workgroup per (batch row, KV head): log-sum-exp merge over
-//                 splits, normalise, un-rotate by R_v (read once for the G heads),
-//                 write fp32 / bf16 / lse (reference :330-336, 366-368).
+//                 workgroup first builds its group's q-side operands (q R_k^T,
+//                 q S^T) in LDS, then owns a contiguous token range of one (batch
+//                 row, KV head), dealt to its waves in 16-token blocks round-robin.
+//                 All G query heads of the GQA group share every K/V byte read
+//                 (reference runtime/triton_kernels.py:84-198 re-reads the tile
+//                 once per query head).
+//   merge_kernel  one workgroup per (batch row, query head): log-sum-exp merge over
+//                 splits, normalise, un-rotate by R_v, write fp32 / bf16 / lse
+//                 (reference :330-336, 366-368).
 //
 // Per 16-token block, lane l = (n = l & 15, g = l >> 4):
 //
@@ -175,12 +176,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
 }
 
 struct Ws {
-    size_t po, pml, img, total;
+    size_t po, pml, total;
 };
 
-// Per-group q-side image written by prep_kernel and read by every split workgroup of the
-// group: the register contents of the key-score and QJL A operands for one wave (lane-major,
-// one 16-byte load per lane and slot), the per-head QJL offsets and the fixed-point scale.
+// Per-group q-side image, built in LDS by every split workgroup of the group: the register
+// contents of the key-score and QJL A operands for one wave (lane-major, one 16-byte read per
+// lane and slot), the per-head QJL offsets and the fixed-point scale.
 constexpr int IMG_QA = 0;                   // [8 j][64 lanes][4]  key-score A operand
 constexpr int IMG_QJ = IMG_QA + 8 * 64 * 4;  // [set][2 jj][64 lanes][4]  QJL A operand (int8 limbs)
 constexpr int IMG_SQ = IMG_QJ + 2 * 2 * 64 * 4;  // [8 heads] sum_d q_proj (fixed-point, as float)
@@ -194,9 +195,7 @@ Ws ws_layout(int batch, int q_heads, int n_split) {
     const size_t bh = (size_t)batch * q_heads;
     w.po = 0;
     w.pml = align256(w.po + bh * (size_t)n_split * D * sizeof(float));
-    w.img = align256(w.pml + bh * (size_t)n_split * 2 * sizeof(float));
-    const size_t groups = (size_t)batch * q_heads;  // >= batch * kv_heads
-    w.total = align256(w.img + groups * IMG_DW * sizeof(uint32_t));
+    w.total = align256(w.pml + bh * (size_t)n_split * 2 * sizeof(float));
     return w;
 }
 
@@ -259,6 +258,7 @@ struct Smem {
         struct {
             uint4 img[IMG_DW / 4];      // this group's q-side image
             uint32_t ksrc[16];          // Ck hi|lo per key code
+            PrepLds<GC> ps;             // scratch of the image builder
         } pro;
         struct {
             float o[NW][NH][D];
@@ -348,10 +348,10 @@ __global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ par
     merge_head(blockIdx.x, true, threadIdx.x, n_split, part_o, part_ml, Rv, out_f32, out_bf16, lse_out, so, part, red);
 }
 
-// ------------------------------------------------------------------ prep kernel
-// One workgroup per (batch row, KV head): q_rot = q R_k^T and q_proj = q S^T for the group's
-// query heads (reference runtime/triton_kernels.py:289, 305-306), split into the MFMA
-// operand layouts the split kernel holds in registers:
+// ------------------------------------------------------------------ q-side image
+// Per (batch row, KV head): q_rot = q R_k^T and q_proj = q S^T for the group's query heads
+// (reference runtime/triton_kernels.py:289, 305-306), split into the MFMA operand layouts the
+// split kernel holds in registers:
 //   key score: lane (n, g), MFMA j, VGPR r = q_x[h][32 g + 4 j + r] twice (bf16), row n =
 //              R::row(h, x), x = 0: bf16(q_rot), x = 1: bf16(q_rot - bf16(q_rot));
 //   QJL:       x_d = rint(q_proj_d 2^(G2 - d % 8)) (negated for d % 8 = 7) in four balanced
@@ -359,8 +359,6 @@ __global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ par
 //              dim 32 g + 4 jj + v + 8 e; sum_d y_d (y_d = x_d 2^(d % 8), exact) per head and
 //              2^(1 - G2), both times the QJL logit scale.  The key-score operand carries the
 //              logit scale times log2 e.
-constexpr int PT = 512;  // prep threads: (matrix, output dim, half of the dot product)
-
 // Balanced base-256 digits of x (|x| < 2^29) into the limb image lb[limb][head][d / 32][d % 8]
 // byte (d / 8) % 4.
 template <int NH>
@@ -491,21 +489,14 @@ __device__ __forceinline__ void build_image(const uint16_t* __restrict__ q, int 
     }
 }
 
-template <bool QJL, int GC>
-__global__ __launch_bounds__(PT) void prep_kernel(const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G,
-                                                  const float* __restrict__ Rk, const float* __restrict__ S,
-                                                  float c_mse, float c_qjl, uint32_t* __restrict__ img) {
-    __shared__ PrepLds<GC> L;
-    build_image<QJL, GC, PT>(q, q_heads, kv_heads, G, blockIdx.x, Rk, S, c_mse, c_qjl, L,
-                                 img + (size_t)blockIdx.x * IMG_DW, threadIdx.x);
-}
 
 template <int KB, int VB, bool QJL, int GC>
 __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
-    const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vn, const uint32_t* __restrict__ qimg,
+    const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vn, const float* __restrict__ Rk,
+    const float* __restrict__ S, float c_mse, float c_qjl,
     const float* __restrict__ Ck, const float* __restrict__ Cv, float scale,
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
     using Sm = Smem<KB, VB, QJL, GC>;
@@ -614,14 +605,13 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     };
 
     // ------------------------------------------------------------ prologue
-    // round 1: codebooks (hi|lo) and the group's q-side image from prep_kernel (one 16-byte
-    // read per thread; every split workgroup of the group reads the same L2-resident bytes)
+    // round 1: codebooks (hi|lo) and the group's q-side image (every split workgroup of the
+    // group computes it: two 128 x 128 mat-vecs per head from L2-resident R_k and S, cheaper
+    // than a separate launch ahead of the split pass)
     if (tid < (1 << KB)) sm.u.pro.ksrc[tid] = pack_hilo(Ck[tid]);
     if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = pack_hilo(Cv[tid - 64]);
-    {
-        const uint4* src = reinterpret_cast<const uint4*>(qimg + (size_t)grp * IMG_DW);
-        for (int i = tid; i < IMG_DW / 4; i += NT) sm.u.pro.img[i] = src[i];
-    }
+    build_image<QJL, GC, NT>(q, q_heads, kv_heads, G, grp, Rk, S, c_mse, c_qjl, sm.u.pro.ps,
+                             reinterpret_cast<uint32_t*>(sm.u.pro.img), tid);
     // zero slots of the weight transpose (never written by the loop)
     for (int i = tid; i < NW * 16 * Sm::WTS; i += NT) (&sm.wt[0][0][0])[i] = 0u;
     __syncthreads();
@@ -937,7 +927,8 @@ struct SplitArgs {
     const uint16_t* kr;
     const uint8_t* vc;
     const uint16_t* vn;
-    const uint32_t* qimg;
+    const float *Rk, *S;
+    float c_mse, c_qjl;
     const float *Ck, *Cv;
     float scale;
     int64_t tps;
@@ -997,7 +988,7 @@ int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out
     if (a.po == nullptr) return TQ_OK;  // sizing query only
     hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC>::NT), 0, s, a.q, a.q_heads,
                        a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
-                       a.vn, a.qimg, a.Ck, a.Cv, a.scale, tps, ns, a.po, a.pml);
+                       a.vn, a.Rk, a.S, a.c_mse, a.c_qjl, a.Ck, a.Cv, a.scale, tps, ns, a.po, a.pml);
     return TQ_OK;
 }
 
@@ -1067,8 +1058,11 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int groups = batch * kv_heads;
-    SplitArgs a{q, q_heads, kv_heads, G, seq_starts, seq_lens, n_tokens, cap, k_codes, k_norms, k_signs, k_rnorms,
-                v_codes, v_norms, nullptr, key_centers, value_centers, scale, 0, 0, nullptr, nullptr};
+    SplitArgs a{q,        q_heads,  kv_heads, G,           seq_starts,    seq_lens,
+                n_tokens, cap,      k_codes,  k_norms,     k_signs,       k_rnorms,
+                v_codes,  v_norms,  key_rotation, qjl,     scale * LOG2E, scale * LOG2E * QJL_SCALE,
+                key_centers, value_centers, scale, 0,      0,             nullptr,
+                nullptr};
     int n_split = 0;
     int64_t tps = 0;
     int st = dispatch(value_bits, has_qjl, G, a, groups, s, &n_split, &tps);  // sizing
@@ -1078,21 +1072,7 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     char* base = static_cast<char*>(workspace);
     a.po = reinterpret_cast<float*>(base + w.po);
     a.pml = reinterpret_cast<float*>(base + w.pml);
-    uint32_t* qimg = reinterpret_cast<uint32_t*>(base + w.img);
-    a.qimg = qimg;
-    // q-side operands once per group, then the split pass, then the merge
-    {
-        const float c_mse = scale * LOG2E, c_qjl = scale * LOG2E * QJL_SCALE;
-        auto prep = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3(groups), dim3(PT), 0, s, q, q_heads, kv_heads, G, key_rotation, qjl, c_mse,
-                               c_qjl, qimg);
-        };
-        if (G <= 4)
-            has_qjl ? prep(prep_kernel<true, 1>) : prep(prep_kernel<false, 1>);
-        else
-            has_qjl ? prep(prep_kernel<true, 2>) : prep(prep_kernel<false, 2>);
-        TQ_CHECK_LAUNCH();
-    }
+    // every split workgroup builds its group's q-side operands, then the merge
     st = dispatch(value_bits, has_qjl, G, a, groups, s, &n_split, &tps);
     if (st != TQ_OK) return st;
     TQ_CHECK_LAUNCH();
