@@ -538,7 +538,9 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     const int64_t t0 = r0;
     const int64_t t1 = r1 > r0 ? r1 : r0;
     const int64_t ntok = t1 - t0;
-    const int64_t step = (int64_t)NW * BLK;
+    // token offsets within the range are 32-bit: the host keeps the range below 2^25 tokens
+    const int nt = (int)ntok;
+    constexpr int STEP = NW * BLK;
     const size_t row0 = (size_t)grp * cap + (size_t)(t0 < n_tokens ? t0 : 0);
 
     // workgroup buffer descriptors over [t0, t1): reads beyond the range return 0
@@ -568,8 +570,8 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         uint32_t kn, kr, vn;  // norms (f16 bits) of token n
         uint32_t vw[4][2];    // value codes of tokens 4 r + g, lane n's dword(s)
     };
-    auto load = [&](Blk& B, int64_t tb) {
-        const int rel = __builtin_amdgcn_readfirstlane((int)(tb - t0));  // scalar block offset
+    auto load = [&](Blk& B, int rel_) {
+        const int rel = __builtin_amdgcn_readfirstlane(rel_);  // scalar block offset
         if constexpr (KB == 1) {
             B.kw[0] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko, rel * KROW, KV_NT);
         } else if constexpr (KB == 2) {
@@ -674,7 +676,7 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     constexpr int KSHIFT = Sm::KC == 32 ? 8 : (Sm::KC == 8 ? 6 : 3);  // log2 bytes per key-table entry row
     const uint32_t klane = 8u * (uint32_t)(lane & (Sm::KC - 1));
 
-    auto process = [&](const Blk& B, int64_t tb) {
+    auto process = [&](const Blk& B, int rel) {
         // ---- key scores: 8 MFMAs over dims 32 g + 4 j + r
         // two independent accumulation chains (even / odd j) halve the dependent MFMA latency
         f32x4 acc_k = f32x4{0.f, 0.f, 0.f, 0.f}, acc_k1 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -709,7 +711,7 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         }
         // ---- scores (log2 domain) of token n for this lane's heads
         // valid tokens of the block: a scalar count, one compare per lane
-        const int nvalid = __builtin_amdgcn_readfirstlane((int)(t1 - tb < BLK ? t1 - tb : BLK));
+        const int nvalid = __builtin_amdgcn_readfirstlane(nt - rel < BLK ? nt - rel : BLK);
         const bool valid = n < nvalid;
         const float knf = tq::f16_to_f32(B.kn);
         const float krf = QJL ? tq::f16_to_f32(B.kr) : 0.0f;
@@ -847,24 +849,24 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     };
 
     // blocks of this wave: wave, wave + NW, ... (scalar count)
-    const int64_t first = (int64_t)wave * BLK;
-    const int nb = first < ntok ? (int)((ntok - first + step - 1) / step) : 0;
+    const int first = wave * BLK;
+    const int nb = first < nt ? (nt - first + STEP - 1) / STEP : 0;
     if (nb > 0) {
         // two of this wave's blocks in flight: while one is processed the next-but-one is
         // loaded into the register set just consumed, so A and Bq alternate without copies
         Blk A, Bq;
-        int64_t tb = t0 + first;
-        load(A, tb);
-        if (nb > 1) load(Bq, tb + step);
+        int rel = first;
+        load(A, rel);
+        if (nb > 1) load(Bq, rel + STEP);
         int i = 0;
         for (; i + 2 <= nb; i += 2) {
-            process(A, tb);
-            if (i + 2 < nb) load(A, tb + 2 * step);
-            process(Bq, tb + step);
-            if (i + 3 < nb) load(Bq, tb + 3 * step);
-            tb += 2 * step;
+            process(A, rel);
+            if (i + 2 < nb) load(A, rel + 2 * STEP);
+            process(Bq, rel + STEP);
+            if (i + 3 < nb) load(Bq, rel + 3 * STEP);
+            rel += 2 * STEP;
         }
-        if (i < nb) process(A, tb);
+        if (i < nb) process(A, rel);
     }
 
     // ------------------------------------------------------------ epilogue
@@ -985,6 +987,9 @@ int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out
     const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC>::NW, &tps);
     *n_split_out = ns;
     *tps_out = tps;
+    // a workgroup's range stays below 2^25 tokens: its byte ranges fit the 31-bit buffer
+    // descriptors and its token offsets fit 32-bit scalars
+    if (tps >= ((int64_t)1 << 25)) return TQ_ERR_UNSUPPORTED;
     if (a.po == nullptr) return TQ_OK;  // sizing query only
     hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC>::NT), 0, s, a.q, a.q_heads,
                        a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
