@@ -713,6 +713,7 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         // valid tokens of the block: a scalar count, one compare per lane
         const int nvalid = __builtin_amdgcn_readfirstlane(nt - rel < BLK ? nt - rel : BLK);
         const bool valid = n < nvalid;
+        // the f16 norms enter v_fma_mix_f32 as they are (no separate conversions)
         const float knf = tq::f16_to_f32(B.kn);
         const float krf = QJL ? tq::f16_to_f32(B.kr) : 0.0f;
         const float vnf = tq::f16_to_f32(B.vn);  // invalid tokens get p = 0 below
@@ -720,7 +721,8 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         bool over = false;
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i) {
-            float v = knf * ((acc_k[2 * i] + acc_k1[2 * i]) + (acc_k[2 * i + 1] + acc_k1[2 * i + 1]));
+            const float ksum = (acc_k[2 * i] + acc_k1[2 * i]) + (acc_k[2 * i + 1] + acc_k1[2 * i + 1]);
+            float v;
             if constexpr (QJL) {
                 // sum_d y_d s_d from the four limb sums (each |.| <= 2^21): pairs exact in int32
                 int lo, hi;
@@ -732,7 +734,9 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
                     hi = acc_q[1][2 * i] + (acc_q[1][2 * i + 1] << 8);
                 }
                 const float qi = __builtin_fmaf((float)hi, 65536.0f, (float)lo);
-                v = __builtin_fmaf(krf, __builtin_fmaf(qi, qfix, -sq[i]), v);
+                v = __builtin_fmaf(knf, ksum, __builtin_fmaf(krf, __builtin_fmaf(qi, qfix, -sq[i]), 0.0f));
+            } else {
+                v = knf * ksum;
             }
             lg[i] = valid ? v : NEG_INF;
             over |= lg[i] > m_thr[i];
@@ -763,7 +767,7 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
         for (int i = 0; i < R::HPL; ++i) {
             const float p = __builtin_amdgcn_exp2f(lg[i] - m_ref[i]);  // m_ref finite once a block is seen
             s_lane[i] += p;
-            const float w = p * vnf;
+            const float w = __builtin_fmaf(vnf, p, 0.0f);  // p, vnf >= 0
             // (hi, hi) by one conversion; hi as fp32 is its high half
             const uint32_t hh = __builtin_bit_cast(uint32_t, bf16x2{(__bf16)w, (__bf16)w});
             wq[i][0] = hh;
