@@ -47,21 +47,19 @@
 namespace {
 
 constexpr int D = TQ_DIM;
-// waves per split workgroup (one workgroup per CU): 4 per SIMD for the paired 4-bit value
-// layout (<= 128 VGPRs), 3 per SIMD for the other layouts with at most 4 query heads per KV
-// head, 2 per SIMD with 5..8
-#ifndef TQ_ATTN_WAVES_P
-#define TQ_ATTN_WAVES_P 16
-#endif
+// waves per split workgroup (one workgroup per CU), the most each kernel's registers allow
+// without spills in its loop: with at most 4 query heads per KV head, 4 per SIMD (<= 128
+// VGPRs) except 3 per SIMD for 3-bit Q_prod values; with 5..8 heads, 3 per SIMD (<= 168)
+// except 2 per SIMD for 3-bit values
 #ifndef TQ_ATTN_WAVES_G4
-#define TQ_ATTN_WAVES_G4 12
+#define TQ_ATTN_WAVES_G4 16
 #endif
 #ifndef TQ_ATTN_WAVES_G8
-#define TQ_ATTN_WAVES_G8 8
+#define TQ_ATTN_WAVES_G8 12
 #endif
-template <int VB, int GC>
+template <int VB, int GC, bool QJL>
 struct Cfg {
-    static constexpr int NW = GC == 1 ? (VB == 4 ? TQ_ATTN_WAVES_P : TQ_ATTN_WAVES_G4) : TQ_ATTN_WAVES_G8;
+    static constexpr int NW = GC == 1 ? ((VB == 3 && QJL) ? 12 : TQ_ATTN_WAVES_G4) : (VB == 3 ? 8 : TQ_ATTN_WAVES_G8);
     static constexpr int NT = NW * 64;
 };
 constexpr int BLK = 16;        // tokens per block (MFMA N)
@@ -241,7 +239,7 @@ struct PrepLds {
 template <int KB, int VB, bool QJL, int GC>
 struct Smem {
     static constexpr int NH = 4 * GC;
-    static constexpr int NW = Cfg<VB, GC>::NW;
+    static constexpr int NW = Cfg<VB, GC, QJL>::NW;
     static constexpr bool PV = PAIRED<VB, GC>;
     static constexpr int WTS = PV ? WT_STRIDE_P : WT_STRIDE;
     // both lookup tables sit below 64 KB, so their base folds into the LDS instruction's offset.
@@ -491,7 +489,7 @@ __device__ __forceinline__ void build_image(const uint16_t* __restrict__ q, int 
 
 
 template <int KB, int VB, bool QJL, int GC>
-__global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
+__global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
@@ -501,8 +499,8 @@ __global__ __launch_bounds__((Cfg<VB, GC>::NT)) void split_kernel(
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
     using Sm = Smem<KB, VB, QJL, GC>;
     using R = Rows<GC>;
-    constexpr int NW = Cfg<VB, GC>::NW;
-    constexpr int NT = Cfg<VB, GC>::NT;
+    constexpr int NW = Cfg<VB, GC, QJL>::NW;
+    constexpr int NT = Cfg<VB, GC, QJL>::NT;
     constexpr int NH = R::NH;
     constexpr int KROW = D * KB / 8;  // bytes per key row
     constexpr int VROW = D * VB / 8;  // bytes per value row
@@ -959,7 +957,7 @@ int wgs_per_cu() {
     static int occ = 0;
     if (occ == 0) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, Cfg<VB, GC>::NT, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, Cfg<VB, GC, QJL>::NT, 0) !=
                 hipSuccess ||
             o < 1)
             o = 1;
@@ -988,14 +986,14 @@ template <int KB, int VB, bool QJL, int GC>
 int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out, int64_t* tps_out) {
     const int target = wgs_per_cu<KB, VB, QJL, GC>() * cu_count();
     int64_t tps;
-    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC>::NW, &tps);
+    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC, QJL>::NW, &tps);
     *n_split_out = ns;
     *tps_out = tps;
     // a workgroup's range stays below 2^25 tokens: its byte ranges fit the 31-bit buffer
     // descriptors and its token offsets fit 32-bit scalars
     if (tps >= ((int64_t)1 << 25)) return TQ_ERR_UNSUPPORTED;
     if (a.po == nullptr) return TQ_OK;  // sizing query only
-    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC>::NT), 0, s, a.q, a.q_heads,
+    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC, QJL>::NT), 0, s, a.q, a.q_heads,
                        a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
                        a.vn, a.Rk, a.S, a.c_mse, a.c_qjl, a.Ck, a.Cv, a.scale, tps, ns, a.po, a.pml);
     return TQ_OK;
