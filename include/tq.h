@@ -135,6 +135,52 @@ int tq_dequantize_prod(const uint8_t* codes, const uint16_t* norms, const uint8_
                        int mse_bits, const float* rotation, const float* centers, const float* qjl,
                        uint16_t* out, void* stream);
 
+/*
+ * Channel groups (the outlier-channel split).  A group is `sub_dim` channels of the
+ * dim-channel head, listed in `channels` (HOST memory, strictly ascending), with its
+ * own sub_dim x sub_dim rotation / QJL matrix, codebook and bit width (1..8).  The
+ * packed rows of a group are ceil(sub_dim*bits/8) code bytes and ceil(sub_dim/8) sign
+ * bytes per token (the layout above with D = sub_dim); they need no alignment.
+ *
+ * Build the group's matrices in channel space once, on the host:
+ *   out[j][channels[i]] = sub[j][i] for i, j < sub_dim;  every other entry 0.
+ * sub is row-major [sub_dim][sub_dim], out is row-major [dim][dim]; both host memory.
+ * Helper for the group-matrix arguments below; no counterpart in the reference, which
+ * gathers tensor[..., channels] instead (runtime/packed_qmse_cache.py:441-442, 484-485).
+ */
+int tq_group_matrix(const float* sub, int sub_dim, const int32_t* channels, int dim, float* out);
+
+/*
+ * Encode one channel group: Q_mse at `bits` when qjl is NULL, else Q_prod keys with
+ * `bits` MSE bits plus the QJL sketch (centers, signs and rnorms then required).
+ * Results are those of tq_quantize_mse / tq_quantize_prod applied to the gathered
+ * sub-vectors x[..., channels] with D = sub_dim.  rotation and qjl are the channel-space
+ * [dim][dim] matrices of tq_group_matrix (device memory).
+ * Replaces reference _encode_split (runtime/packed_qmse_cache.py:481-496) and
+ * _encode_keys_split_qjl (:437-454), one group per call.
+ */
+int tq_quantize_group(const uint16_t* x, int batch, int heads, int64_t tokens, int dim,
+                      int64_t x_sb, int64_t x_sh, int64_t x_st,
+                      const int32_t* channels, int sub_dim, int bits,
+                      const float* rotation, const float* centers, const float* boundaries, const float* qjl,
+                      uint8_t* codes, uint16_t* norms, uint8_t* signs, uint16_t* rnorms,
+                      int64_t out_cap, int64_t out_offset, void* stream);
+
+/*
+ * Decode one channel group into the bf16 rows out [groups*tokens][dim] (16-byte
+ * aligned): the group's channels get tq_dequantize_mse / tq_dequantize_prod of the
+ * sub-vector (QJL correction when qjl is non-NULL, scaled by sqrt(pi/2)/sub_dim); the
+ * other channels are zeroed, or kept when `merge` is non-zero.  Decoding the normal
+ * group, then the outlier group with merge = 1, gives the full row.
+ * Replaces reference _decode_merge (runtime/packed_qmse_cache.py:498-515) and
+ * _decode_keys_merge_qjl (:456-479), one group per call.
+ */
+int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
+                        const uint16_t* rnorms, int64_t groups, int64_t tokens, int64_t cap, int dim,
+                        const int32_t* channels, int sub_dim, int bits,
+                        const float* rotation, const float* centers, const float* qjl,
+                        int merge, uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

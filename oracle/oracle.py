@@ -20,11 +20,25 @@ Contents
   ``runtime/packed_qmse_cache.py:312-330``) and V to dense fp64 vectors, then
   plain softmax attention.  Agreement of the two pins the rotation algebra.
 
+* ``split_dequant_f64`` / ``dense_attention_f64`` / ``split_fused_attention_f64`` --
+  the outlier-split layer (two channel groups): its fp64 dequantisation, plain
+  attention over dense rows, and the fused formula summed over the groups.
+  The split encoder itself is ``encode_mse`` / ``encode_prod`` at D = d applied
+  to the gathered sub-vectors x[..., channels].
+
 Parity status of each function is pinned by tests/test_oracle_*.py:
   encode_mse / encode_prod  -- reference golden vectors (tie-band), brute force
   pack_codes / unpack_codes -- hand-computed bytes, golden vectors, round trip
   fused_attention_f64       -- dequant_attention_f64 identity, golden chunked
                                output of the reference, LSE-merge identity
+  encode_* at D = d < 128   -- tie-band against the torch restatement of the
+                               reference (itself bit-exact on the golden vectors),
+                               nearest-centroid brute force
+  split_dequant_f64         -- the torch restatement's decode_merge (bf16) to
+                               within its roundings
+  split_fused_attention_f64 -- identity with dense_attention_f64 over
+                               split_dequant_f64; one group of all D channels
+                               reduces to fused_attention_f64
 """
 
 from __future__ import annotations
@@ -288,6 +302,77 @@ def dequant_attention_f64(q_bf16, layer: dict) -> np.ndarray:
                 lg = khat @ q[b, h * g + j] / math.sqrt(D)
                 p = np.exp(lg - lg.max())
                 out[b, h * g + j] = (p @ vhat) / p.sum()
+    return out
+
+
+# ------------------------------------------------------------ channel groups
+def split_dequant_f64(groups: list[dict], full_dim: int) -> tuple[np.ndarray, np.ndarray]:
+    """fp64 K^ and V^ [B,Hkv,N,full_dim] of an outlier-split layer, unrounded: each group
+    (a ``dequant_layer_f64`` dict of its own dimension plus ``channels``) decoded and
+    scattered to its channels (reference _decode_merge / _decode_keys_merge_qjl,
+    runtime/packed_qmse_cache.py:456-515, without the bf16 roundings)."""
+    B, Hkv, N = groups[0]["kcodes"].shape[:3]
+    kh = np.zeros((B, Hkv, N, full_dim))
+    vh = np.zeros((B, Hkv, N, full_dim))
+    for g in groups:
+        k, v = dequant_layer_f64(g)
+        kh[..., g["channels"]] = k
+        vh[..., g["channels"]] = v
+    return kh, vh
+
+
+def dense_attention_f64(q_bf16, keys: np.ndarray, values: np.ndarray, n_start=None, n_valid=None) -> np.ndarray:
+    """softmax(q . K / sqrt(D)) V in fp64 over dense [B,Hkv,N,D] rows; query head h reads
+    KV head h // (Hq/Hkv); row b attends to [n_start[b], n_valid[b]) (empty -> 0)."""
+    q = bf16_bits_to_f32(np.asarray(q_bf16)).astype(np.float64)
+    B, Hq, D = q.shape
+    Hkv, N = keys.shape[1], keys.shape[2]
+    g = Hq // Hkv
+    out = np.zeros((B, Hq, D))
+    for b in range(B):
+        lo = 0 if n_start is None else int(n_start[b])
+        hi = N if n_valid is None else int(n_valid[b])
+        if hi <= lo:
+            continue
+        for h in range(Hq):
+            k = keys[b, h // g, lo:hi].astype(np.float64)
+            lg = k @ q[b, h] / math.sqrt(D)
+            p = np.exp(lg - lg.max())
+            out[b, h] = (p @ values[b, h // g, lo:hi].astype(np.float64)) / p.sum()
+    return out
+
+
+def split_fused_attention_f64(q_bf16, groups: list[dict], full_dim: int) -> np.ndarray:
+    """The fused formula over channel groups, in fp64 and in each group's rotated space:
+    logit_t = sum_g (n_g <q[ch_g] R_k,g^T, C_k,g[kidx]> + sqrt(pi/2)/d_g rho_g <q[ch_g] S_g^T, s>) / sqrt(D),
+    out[ch_g] = (sum_t p_t n_v,g C_v,g[vidx]) R_v,g / sum_t p_t."""
+    q = bf16_bits_to_f32(np.asarray(q_bf16)).astype(np.float64)
+    B, Hq, D = q.shape
+    Hkv, N = groups[0]["kcodes"].shape[1:3]
+    G = Hq // Hkv
+    out = np.zeros((B, Hq, full_dim))
+    for b in range(B):
+        for h in range(Hkv):
+            qq = q[b, h * G:(h + 1) * G]
+            logits = np.zeros((G, N))
+            for g in groups:
+                d, ch = len(g["channels"]), g["channels"]
+                kidx = unpack_codes(g["kcodes"][b, h], g["kbits"], d)
+                kn = f16_bits_to_f32(g["knorms"][b, h]).astype(np.float64)
+                logits += ((qq[:, ch] @ g["Rk"].astype(np.float64).T) @ g["Ck"].astype(np.float64)[kidx].T) * kn
+                if g.get("signs") is not None:
+                    sg = _sign_pm1(g["signs"][b, h], d)
+                    rn = f16_bits_to_f32(g["rnorms"][b, h]).astype(np.float64)
+                    logits += math.sqrt(math.pi / 2) / d * rn * ((qq[:, ch] @ g["S"].astype(np.float64).T) @ sg.T)
+            logits /= math.sqrt(D)
+            p = np.exp(logits - logits.max(axis=1, keepdims=True))
+            ssum = p.sum(axis=1, keepdims=True)
+            for g in groups:
+                d, ch = len(g["channels"]), g["channels"]
+                vidx = unpack_codes(g["vcodes"][b, h], g["vbits"], d)
+                vn = f16_bits_to_f32(g["vnorms"][b, h]).astype(np.float64)
+                o_rot = (p * vn) @ g["Cv"].astype(np.float64)[vidx]
+                out[b, h * G:(h + 1) * G][:, ch] = (o_rot / ssum) @ g["Rv"].astype(np.float64)
     return out
 
 

@@ -13,6 +13,9 @@ torch build it reproduces the reference's bits:
   encode_keys_qjl_group   runtime/packed_qmse_cache.py:285-310, 148-154
   decode_keys_qjl_group   runtime/packed_qmse_cache.py:312-330
   chunked_attention       runtime/attention.py:189-304 (packed history only)
+  detect_outlier_channels runtime/packed_qmse_cache.py:95-114
+  encode_split            runtime/packed_qmse_cache.py:481-496 (+ :437-454 for Q_prod keys)
+  decode_merge            runtime/packed_qmse_cache.py:498-515 (+ :456-479 for Q_prod keys)
 
 Pinned by tests/test_oracle_golden.py against the reference's own outputs.
 """
@@ -150,3 +153,41 @@ def encode_layer(k: torch.Tensor, v: torch.Tensor, params: dict, use_qjl: bool, 
         out["signs"] = out["rnorms"] = None
     out["values"] = encode_group(v, params["Rv"], params["Cv"], params["Bv"], bits)
     return out
+
+
+def detect_outlier_channels(k: torch.Tensor, v: torch.Tensor, n: int) -> tuple[torch.Tensor, torch.Tensor]:
+    combined = k.float().pow(2).sum(dim=(0, 1, 2)) + v.float().pow(2).sum(dim=(0, 1, 2))
+    _, top = torch.topk(combined, n)
+    outlier = top.sort().values
+    mask = torch.ones(k.shape[-1], dtype=torch.bool)
+    mask[outlier] = False
+    return outlier, torch.arange(k.shape[-1])[mask]
+
+
+def encode_split(x: torch.Tensor, groups: list[dict], use_qjl: bool) -> list[dict]:
+    """Each group dict holds ``idx`` (channels), ``R``, ``C``, ``B``, ``bits`` (MSE bits) and,
+    for Q_prod keys, ``S``.  Returns per group {"packed", "signs", "rnorms"}."""
+    out = []
+    for g in groups:
+        sub = x[..., g["idx"]]
+        if use_qjl:
+            mse, signs, rn = encode_keys_qjl_group(sub, g["R"], g["C"], g["B"], g["bits"], g["S"])
+            out.append({"packed": mse, "signs": signs, "rnorms": rn})
+        else:
+            out.append({"packed": encode_group(sub, g["R"], g["C"], g["B"], g["bits"]), "signs": None,
+                        "rnorms": None})
+    return out
+
+
+def decode_merge(encoded: list[dict], groups: list[dict], full_dim: int) -> torch.Tensor:
+    parts = []
+    for e, g in zip(encoded, groups):
+        if e["signs"] is not None:
+            parts.append(decode_keys_qjl_group(e["packed"], e["signs"], e["rnorms"], g["R"], g["C"], g["S"]))
+        else:
+            parts.append(decode_group(e["packed"], g["R"], g["C"]))
+    b, h, n = parts[0].shape[:3]
+    full = torch.zeros(b, h, n, full_dim, dtype=parts[0].dtype)
+    for part, g in zip(parts, groups):
+        full[..., g["idx"]] = part
+    return full

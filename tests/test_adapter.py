@@ -62,8 +62,8 @@ def test_activate_banner_and_errors(capsys):
     model.config._name_or_path = ""
     with pytest.raises(ValueError, match="tokenizer"):
         turboquant.activate(model, None, quiet=True)
-    with pytest.raises(NotImplementedError):
-        turboquant.activate(model, CharTokenizer(), num_outlier_channels=4, quiet=True)
+    with pytest.raises(ValueError, match="outlier bits"):
+        turboquant.activate(model, CharTokenizer(), num_outlier_channels=4, outlier_extra_bits=5, quiet=True)
     model.config.use_cache = False
     with pytest.raises(ValueError, match="not compatible"):
         turboquant.activate(model, CharTokenizer(), quiet=True)
@@ -122,8 +122,8 @@ def test_cache_layer_protocol_without_data():
     assert layer.get_seq_length() == 0 and layer.get_max_length() == -1
     assert layer.get_mask_sizes(1) == (1, 0)
     assert layer.keys_packed is None and layer._keys_qjl is None and layer.storage_bytes() == 0
-    with pytest.raises(NotImplementedError):
-        PackedMSELayer(bits=4, num_outlier_channels=2)
+    split = PackedMSELayer(bits=4, num_outlier_channels=2)
+    assert split._keys_outlier is None and split._keys_outlier_qjl is None and not split._outlier_enabled
 
 
 def test_valid_range_from_masks():

@@ -1,0 +1,310 @@
+"""Outlier-channel split on the GPU: libtq's channel-group encoder and decoder are
+bit-identical to the CPU oracle run at D = d on the gathered sub-vectors (the oracle is
+pinned at d < 128 in tests/test_oracle_split.py), and the split layer's decode
+attention matches fp64 attention over the same decoded rows."""
+
+import numpy as np
+import pytest
+import torch
+
+import turboquant
+from oracle import oracle as O
+from turboquant.quantization.turboquant_mse import codebook_f32
+from turboquant.runtime import kernels as K
+from turboquant.runtime.attention import fused_attention
+from turboquant.runtime.packed_qmse_cache import PackedMSELayer
+from turboquant.runtime.params import split_codecs
+from turboquant.runtime.synthetic import kv_bf16, query_bf16
+
+from ._tiny_model import CharTokenizer, tiny_llama
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+TOL = 2e-3
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _host(g):
+    return g.rotation.cpu().numpy(), g.centers.cpu().numpy(), g.boundaries.cpu().numpy()
+
+
+def _with_specials(x: torch.Tensor, ch: np.ndarray) -> torch.Tensor:
+    """Append rows that are zero on the group, nonzero only outside it, tiny, huge and
+    one-hot inside it."""
+    B, H = x.shape[:2]
+    s = torch.zeros(5, D)
+    outside = np.setdiff1d(np.arange(D), ch)
+    s[1, outside] = 3.0  # zero on the group: stored norm 1.0, middle codes
+    s[2, ch] = 1e-3
+    s[3, ch] = 3000.0 / len(ch) ** 0.5
+    s[4, ch[-1]] = -5.0
+    return torch.cat([x, s.to(torch.bfloat16).to(x.device).expand(B, H, 5, D)], dim=2)
+
+
+def _channels(d: int, seed: int) -> np.ndarray:
+    return np.sort(np.random.default_rng(seed).choice(D, d, replace=False))
+
+
+@pytest.mark.parametrize("d,extra", [(3, 4), (8, 1), (13, 4), (40, 2)])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_quantize_group_mse_bit_exact(cuda, d, extra, bits):
+    """Both groups of a split (the outlier group at bits + extra, up to 8 bits) at a token
+    offset inside a larger capacity: codes and norms equal the oracle on x[..., ch]."""
+    outl = _channels(d, 10 * d + bits)
+    sc = split_codecs(np.setdiff1d(np.arange(D), outl), outl, bits, extra, 0, False, cuda)
+    x = _with_specials(kv_bf16((2, 3, 131, D), seed=bits + d, device=cuda, outlier_channels=2), outl)
+    n = x.shape[2]
+    cap, off = n + 7, 4
+    for g in (sc.value_normal, sc.value_outlier):
+        codes = torch.zeros(2, 3, cap, K.row_bytes(g.dim, g.bits), dtype=torch.uint8, device=cuda)
+        norms = torch.zeros(2, 3, cap, dtype=torch.float16, device=cuda)
+        K.quantize_group(x, g, codes, norms, offset=off)
+        torch.cuda.synchronize()
+        R, _, bnd = _host(g)
+        rc, rn = O.encode_mse(u16(x).reshape(-1, D)[:, g.channels], g.bits, R, bnd)
+        got = codes[:, :, off:off + n].cpu().numpy().reshape(rc.shape)
+        assert np.array_equal(got, rc), f"{g.dim} ch, {g.bits} bits: {(got != rc).sum()} code bytes differ"
+        assert np.array_equal(u16(norms[:, :, off:off + n]).reshape(-1), rn)
+        assert int(codes[:, :, :off].count_nonzero()) == 0 and int(codes[:, :, off + n:].count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("d,bits,extra", [(4, 2, 1), (8, 4, 1), (13, 3, 4), (40, 4, 2)])
+def test_quantize_group_prod_bit_exact(cuda, d, bits, extra):
+    outl = _channels(d, d + bits)
+    sc = split_codecs(np.setdiff1d(np.arange(D), outl), outl, bits, extra, 3, True, cuda)
+    x = _with_specials(kv_bf16((2, 2, 97, D), seed=50 + d, device=cuda), outl)
+    B, H, n, _ = x.shape
+    for g in (sc.key_normal, sc.key_outlier):
+        codes = torch.zeros(B, H, n, K.row_bytes(g.dim, g.bits), dtype=torch.uint8, device=cuda)
+        norms = torch.zeros(B, H, n, dtype=torch.float16, device=cuda)
+        signs = torch.zeros(B, H, n, K.row_bytes(g.dim, 1), dtype=torch.uint8, device=cuda)
+        rnorms = torch.zeros(B, H, n, dtype=torch.float16, device=cuda)
+        K.quantize_group(x, g, codes, norms, signs, rnorms)
+        torch.cuda.synchronize()
+        R, C, bnd = _host(g)
+        rc, rn, rs, rr = O.encode_prod(u16(x).reshape(-1, D)[:, g.channels], g.bits, R, C, bnd, g.qjl.cpu().numpy())
+        assert np.array_equal(codes.cpu().numpy().reshape(rc.shape), rc), (g.dim, g.bits)
+        assert np.array_equal(u16(norms).reshape(-1), rn)
+        got_s = signs.cpu().numpy().reshape(rs.shape)
+        assert np.array_equal(got_s, rs), f"{(got_s != rs).sum()} sign bytes differ ({g.dim} ch)"
+        assert np.array_equal(u16(rnorms).reshape(-1), rr)
+
+
+def test_quantize_group_strided_input_and_decode_append(cuda):
+    base = kv_bf16((1, 4, 3, D), seed=7, device=cuda)
+    x = base.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)  # [B,H,T,D] view of a [B,T,H,D] buffer
+    assert not x.is_contiguous()
+    outl = np.array([5, 6, 70, 71, 127])
+    sc = split_codecs(np.setdiff1d(np.arange(D), outl), outl, 4, 2, 0, True, cuda)
+    g = sc.key_outlier
+    B, H, T, _ = x.shape
+    bufs = [torch.zeros(B, H, T, K.row_bytes(5, g.bits), dtype=torch.uint8, device=cuda),
+            torch.zeros(B, H, T, dtype=torch.float16, device=cuda),
+            torch.zeros(B, H, T, 1, dtype=torch.uint8, device=cuda),
+            torch.zeros(B, H, T, dtype=torch.float16, device=cuda)]
+    K.quantize_group(x[:, :, :1], g, *bufs, offset=0)
+    for t in range(1, T):
+        K.quantize_group(x[:, :, t:t + 1], g, *bufs, offset=t)
+    torch.cuda.synchronize()
+    R, C, bnd = _host(g)
+    rc, rn, rs, rr = O.encode_prod(u16(x).reshape(-1, D)[:, outl], g.bits, R, C, bnd, g.qjl.cpu().numpy())
+    assert np.array_equal(bufs[0].cpu().numpy().reshape(rc.shape), rc)
+    assert np.array_equal(bufs[2].cpu().numpy().reshape(rs.shape), rs)
+    assert np.array_equal(u16(bufs[1]).reshape(-1), rn) and np.array_equal(u16(bufs[3]).reshape(-1), rr)
+
+
+@pytest.mark.parametrize("qjl", [False, True])
+def test_dequantize_groups_merge_into_full_rows(cuda, qjl):
+    """Normal group (merge=0), then outlier group (merge=1): the full bf16 row equals the
+    oracle's per-group decode scattered to the channels; merge=0 zeroes the other channels."""
+    outl = _channels(9, 3)
+    sc = split_codecs(np.setdiff1d(np.arange(D), outl), outl, 4, 1, 0, qjl, cuda)
+    x = kv_bf16((1, 2, 150, D), seed=9, device=cuda, outlier_channels=3)
+    B, H, N, _ = x.shape
+    out = torch.full((B, H, N, D), 7.0, dtype=torch.bfloat16, device=cuda)
+    ref = np.zeros((B * H * N, D), np.uint16)
+    for gi, g in enumerate((sc.key_normal, sc.key_outlier)):
+        codes = torch.zeros(B, H, N + 3, K.row_bytes(g.dim, g.bits), dtype=torch.uint8, device=cuda)
+        norms = torch.zeros(B, H, N + 3, dtype=torch.float16, device=cuda)
+        extra = {}
+        if qjl:
+            extra = dict(signs=torch.zeros(B, H, N + 3, K.row_bytes(g.dim, 1), dtype=torch.uint8, device=cuda),
+                         rnorms=torch.zeros(B, H, N + 3, dtype=torch.float16, device=cuda))
+        K.quantize_group(x, g, codes, norms, extra.get("signs"), extra.get("rnorms"))
+        K.dequantize_group(codes, norms, N, g, out, merge=gi == 1, **extra)
+        if gi == 0:
+            torch.cuda.synchronize()
+            assert not u16(out).reshape(-1, D)[:, outl].any()  # merge=0 zeroed the other group's channels
+        R, C, _ = _host(g)
+        hc = codes[:, :, :N].cpu().numpy().reshape(B * H * N, -1)
+        hn = u16(norms[:, :, :N]).reshape(-1)
+        if qjl:
+            dec = O.decode_prod(hc, hn, extra["signs"][:, :, :N].cpu().numpy().reshape(B * H * N, -1),
+                                u16(extra["rnorms"][:, :, :N]).reshape(-1), g.bits, g.dim, R, C, g.qjl.cpu().numpy())
+        else:
+            dec = O.decode_mse(hc, hn, g.bits, g.dim, R, C)
+        ref[:, g.channels] = dec
+    torch.cuda.synchronize()
+    assert np.array_equal(u16(out).reshape(-1, D), ref)
+    # the group encodes stay faithful: outlier channels reconstruct to a cosine > 0.97
+    xf = x.float().reshape(-1, D)[:, torch.from_numpy(outl).to(cuda)]
+    of = out.float().reshape(-1, D)[:, torch.from_numpy(outl).to(cuda)]
+    assert torch.nn.functional.cosine_similarity(xf, of, dim=-1).mean().item() > 0.97
+
+
+def _host_groups(layer: PackedMSELayer) -> list[dict]:
+    """Per-group numpy views of a split layer, in the form the fp64 oracle takes."""
+    s, sc, n = layer._store, layer._split, layer.packed_seq_length()
+    out = []
+    for sfx, kg, vg in (("", sc.key_normal, sc.value_normal), ("o", sc.key_outlier, sc.value_outlier)):
+        qjl = kg.qjl is not None
+        out.append({"channels": kg.channels.astype(np.int64),
+                    "kcodes": getattr(s, "kc" + sfx)[:, :, :n].cpu().numpy(),
+                    "knorms": u16(getattr(s, "kn" + sfx)[:, :, :n]),
+                    "vcodes": getattr(s, "vc" + sfx)[:, :, :n].cpu().numpy(),
+                    "vnorms": u16(getattr(s, "vn" + sfx)[:, :, :n]),
+                    "signs": getattr(s, "ks" + sfx)[:, :, :n].cpu().numpy() if qjl else None,
+                    "rnorms": u16(getattr(s, "kr" + sfx)[:, :, :n]) if qjl else None,
+                    "Rk": kg.rotation.cpu().numpy(), "Ck": kg.centers.cpu().numpy(), "kbits": kg.bits,
+                    "Rv": vg.rotation.cpu().numpy(), "Cv": vg.centers.cpu().numpy(), "vbits": vg.bits,
+                    "S": kg.qjl.cpu().numpy() if qjl else None})
+    return out
+
+
+def _oracle_rows(layer: PackedMSELayer) -> tuple[np.ndarray, np.ndarray]:
+    """bf16 K^ / V^ rows (as fp64) decoded by the oracle group by group and scattered."""
+    B, H, _ = layer._shape
+    n = layer.packed_seq_length()
+    kk = np.zeros((B * H * n, D), np.uint16)
+    vv = np.zeros((B * H * n, D), np.uint16)
+    for g in _host_groups(layer):
+        d = len(g["channels"])
+        kc, kn = g["kcodes"].reshape(B * H * n, -1), g["knorms"].reshape(-1)
+        if g["signs"] is not None:
+            kd = O.decode_prod(kc, kn, g["signs"].reshape(B * H * n, -1), g["rnorms"].reshape(-1), g["kbits"], d,
+                               g["Rk"], g["Ck"], g["S"])
+        else:
+            kd = O.decode_mse(kc, kn, g["kbits"], d, g["Rk"], g["Ck"])
+        kk[:, g["channels"]] = kd
+        vv[:, g["channels"]] = O.decode_mse(g["vcodes"].reshape(B * H * n, -1), g["vnorms"].reshape(-1), g["vbits"],
+                                            d, g["Rv"], g["Cv"])
+    f = lambda a: O.bf16_bits_to_f32(a).astype(np.float64).reshape(B, H, n, D)  # noqa: E731
+    return f(kk), f(vv)
+
+
+@pytest.mark.parametrize("qjl,bits", [(True, 4), (False, 3)])
+def test_split_layer_prefill_append_and_attention(cuda, qjl, bits):
+    """Prefill + lazy decode-append of a split layer: packed groups bit-exact against the
+    oracle encoder; attention equals fp64 attention over the same decoded bf16 rows, and
+    lies within a bf16-rounding band of the unrounded fused formula over the groups."""
+    B, Hq, Hkv, N, T = 2, 8, 2, 333, 3
+    k = kv_bf16((B, Hkv, N + T, D), seed=21, device=cuda, outlier_channels=4)
+    v = kv_bf16((B, Hkv, N + T, D), seed=22, device=cuda)
+    layer = PackedMSELayer(bits=bits, num_outlier_channels=4, use_qjl_keys=qjl, quantize_decode=True)
+    layer.initialize_from_dense(k[:, :, :N], v[:, :, :N])
+    layer._lazy_update = True
+    for t in range(N, N + T):
+        layer.update(k[:, :, t:t + 1], v[:, :, t:t + 1])
+    assert layer._outlier_indices.tolist() == [0, 1, 2, 3]  # kv_bf16 plants the outliers at 0..3
+    assert layer.packed_seq_length() == N + T
+    xs_k, xs_v = u16(k).reshape(-1, D), u16(v).reshape(-1, D)
+    for g in _host_groups(layer):
+        ch, d = g["channels"], len(g["channels"])
+        _, bk = codebook_f32(d, g["kbits"])
+        _, bv = codebook_f32(d, g["vbits"])
+        if g["signs"] is not None:
+            rc, rn, rs, rr = O.encode_prod(xs_k[:, ch], g["kbits"], g["Rk"], g["Ck"], bk, g["S"])
+            assert np.array_equal(g["signs"].reshape(rs.shape), rs) and np.array_equal(g["rnorms"].reshape(-1), rr)
+        else:
+            rc, rn = O.encode_mse(xs_k[:, ch], g["kbits"], g["Rk"], bk)
+        assert np.array_equal(g["kcodes"].reshape(rc.shape), rc) and np.array_equal(g["knorms"].reshape(-1), rn)
+        vc, vn = O.encode_mse(xs_v[:, ch], g["vbits"], g["Rv"], bv)
+        assert np.array_equal(g["vcodes"].reshape(vc.shape), vc) and np.array_equal(g["vnorms"].reshape(-1), vn)
+    # the layer's decoded rows are the oracle's
+    kh, vh = _oracle_rows(layer)
+    assert np.array_equal(O.bf16_bits_to_f32(u16(layer._decode_keys_full())).astype(np.float64), kh)
+    assert np.array_equal(O.bf16_bits_to_f32(u16(layer._decode_values_full())).astype(np.float64), vh)
+    q = query_bf16(B, Hq, D, seed=23, device=cuda)
+    out = fused_attention(q.float().unsqueeze(2), layer, Hq // Hkv)[:, :, 0].cpu().numpy()  # fp32 query -> fp32 out
+    ref = O.dense_attention_f64(u16(q), kh, vh)
+    assert np.abs(out - ref).max() <= 1e-5 * np.abs(ref).max()
+    fused = O.split_fused_attention_f64(u16(q), _host_groups(layer), D)
+    assert np.abs(out - fused).max() <= 3e-2 * np.abs(fused).max()
+    # bf16 query in, bf16 out
+    ob = fused_attention(q.unsqueeze(2), layer, Hq // Hkv)
+    assert ob.dtype == torch.bfloat16
+    assert np.abs(ob[:, :, 0].float().cpu().numpy() - ref).max() <= (1e-5 + 2 ** -8) * np.abs(ref).max()
+
+
+def test_split_layer_dense_buffer_and_left_padding(cuda):
+    """quantize_decode=False keeps generated tokens dense after the split history; a
+    left-padded batch attends to its own valid slots only."""
+    B, Hq, Hkv, N, nd = 3, 8, 2, 210, 4
+    k = kv_bf16((B, Hkv, N + nd, D), seed=31, device=cuda, outlier_channels=4)
+    v = kv_bf16((B, Hkv, N + nd, D), seed=32, device=cuda)
+    layer = PackedMSELayer(bits=4, num_outlier_channels=6, use_qjl_keys=True, quantize_decode=False)
+    layer.initialize_from_dense(k[:, :, :N], v[:, :, :N])
+    layer._lazy_update = True
+    for t in range(N, N + nd):
+        layer.update(k[:, :, t:t + 1], v[:, :, t:t + 1])
+    assert layer.packed_seq_length() == N and layer.get_seq_length() == N + nd
+    pad = [0, 17, 150]
+    mask = torch.ones(B, N + nd, dtype=torch.bool, device=cuda)
+    for b, p in enumerate(pad):
+        mask[b, :p] = False
+    q = query_bf16(B, Hq, D, seed=33, device=cuda)
+    out = fused_attention(q.float().unsqueeze(2), layer, Hq // Hkv, mask[:, None, None, :])[:, :, 0].cpu().numpy()
+    kh, vh = _oracle_rows(layer)
+    kk = np.concatenate([kh, O.bf16_bits_to_f32(u16(k[:, :, N:])).astype(np.float64)], axis=2)
+    vv = np.concatenate([vh, O.bf16_bits_to_f32(u16(v[:, :, N:])).astype(np.float64)], axis=2)
+    ref = O.dense_attention_f64(u16(q), kk, vv, n_start=np.array(pad))
+    assert np.abs(out - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_split_full_size_c2_layer_subsample(cuda):
+    """A BASELINE config-2-sized key layer (B=8, Hkv=8, N=32768) split 124 + 4 channels,
+    4-bit Q_prod: a random 2048-vector subsample of both groups is bit-exact against the
+    oracle; every stored norm is |x[..., ch]| to fp16 rounding."""
+    B, H, N = 8, 8, 32768
+    x = kv_bf16((B, H, N, D), seed=2025, device=cuda, outlier_channels=4)
+    outl = np.arange(4)
+    sc = split_codecs(np.arange(4, D), outl, 4, 1, 0, True, cuda)
+    idx = torch.randperm(B * H * N, generator=torch.Generator().manual_seed(6))[:2048]
+    xs = u16(x).reshape(-1, D)[idx.numpy()]
+    for g in (sc.key_normal, sc.key_outlier):
+        rb, sb = K.row_bytes(g.dim, g.bits), K.row_bytes(g.dim, 1)
+        codes = torch.empty(B, H, N, rb, dtype=torch.uint8, device=cuda)
+        norms = torch.empty(B, H, N, dtype=torch.float16, device=cuda)
+        signs = torch.empty(B, H, N, sb, dtype=torch.uint8, device=cuda)
+        rnorms = torch.empty(B, H, N, dtype=torch.float16, device=cuda)
+        K.quantize_group(x, g, codes, norms, signs, rnorms)
+        torch.cuda.synchronize()
+        ch_t = torch.from_numpy(g.channels.astype(np.int64)).to(cuda)
+        ref_norm = x.float()[..., ch_t].norm(dim=-1)
+        assert ((norms.float() - ref_norm).abs() / ref_norm).max().item() < 1e-3
+        R, C, bnd = _host(g)
+        rc, rn, rs, rr = O.encode_prod(xs[:, g.channels], g.bits, R, C, bnd, g.qjl.cpu().numpy())
+        assert np.array_equal(codes.view(-1, rb)[idx.to(cuda)].cpu().numpy(), rc)
+        assert np.array_equal(u16(norms).reshape(-1)[idx.numpy()], rn)
+        assert np.array_equal(signs.view(-1, sb)[idx.to(cuda)].cpu().numpy(), rs)
+        assert np.array_equal(u16(rnorms).reshape(-1)[idx.numpy()], rr)
+
+
+def test_activate_generate_with_outlier_split(cuda):
+    """activate(num_outlier_channels=4) end to end: every packed layer is split, decode
+    tokens are appended to both groups and the storage counts both groups."""
+    model = tiny_llama(device=cuda, dtype=torch.bfloat16)
+    turboquant.activate(model, CharTokenizer(), bits=4, num_outlier_channels=4, quiet=True)
+    ids = torch.randint(0, 94, (1, 150), generator=torch.Generator().manual_seed(2)).to(cuda)
+    out = model.generate(ids, max_new_tokens=6)
+    assert out.shape == (1, 156) and torch.equal(out[0, :150], ids[0])
+    t = turboquant.last_telemetry(model)
+    # per token-kvhead: normal 124 ch (3-bit codes 47 B + 2, signs 16 B + 2, 4-bit values 62 B + 2)
+    # + outlier 4 ch (4-bit codes 2 B + 2, signs 1 B + 2, 5-bit values 3 B + 2)
+    per_tok = (47 + 2 + 16 + 2 + 62 + 2) + (2 + 2 + 1 + 2 + 3 + 2)
+    assert t["packed_actual_bytes"] == 2 * 2 * 150 * per_tok
+    turboquant.deactivate(model, quiet=True)

@@ -1,0 +1,347 @@
+// tq_group.hip -- channel-group (outlier split) encoder and decoder kernels for gfx950.
+//
+// A channel group is a sorted subset of the D = 128 head channels with its own
+// rotation, codebook, bit width (1..8) and, for Q_prod keys, QJL matrix, all of the
+// group's dimension d.  Reference: PackedMSELayer._encode_split /
+// _encode_keys_split_qjl (runtime/packed_qmse_cache.py:481-496, 437-454) gather
+// tensor[..., idx] and run _encode_group / _encode_keys_qjl_group (:376-402,
+// :285-310) on the d-dimensional sub-vectors; _decode_merge / _decode_keys_merge_qjl
+// (:498-515, :456-479) decode each group (:404-435, :312-330) and scatter it back
+// into the full row.
+//
+// The kernels never gather.  One lane owns one token vector and holds the whole
+// 128-channel row with the channels outside the group set to zero; the group's d x d
+// matrices arrive in channel space (tq_group_matrix: row j < d carries the group
+// matrix row j at the group's channels, every other entry 0).  Every fp32 reduction is
+// an fma chain over the channels in ascending order, the group's channels ascend, and
+// an fma whose product is zero returns its addend (up to the sign of a zero sum), so
+// each chain equals the chain over the gathered d-dimensional sub-vector term for
+// term.  Rows j >= d are skipped.  Codes, norms, signs and the decoded values are
+// therefore bit-identical to the plain encoder / decoder run at D = d on the gathered
+// sub-vectors, which is how the CPU oracle states them.
+//
+// Packed rows are ceil(d*bits/8) code bytes and ceil(d/8) sign bytes per token, LSB
+// first, zero padded (runtime/packed_qmse_cache.py:13-43, 148-154); lanes write them
+// byte by byte, so no alignment is required of those buffers.
+
+#include <math.h>
+
+#include "tq_common.h"
+
+namespace {
+
+constexpr int D = TQ_DIM;
+constexpr int GBLOCK = 256;  // lanes (= vectors) per workgroup
+constexpr int MAX_BITS = 8;
+
+// Channel c is in the group iff bit c is set.  Passed by value: uniform (SGPR) words,
+// and with c a compile-time constant after unrolling each test is a scalar bit test.
+struct ChanMask {
+    uint32_t w[D / 32];
+};
+
+__device__ __forceinline__ bool in_group(const ChanMask& m, int c) { return (m.w[c >> 5] >> (c & 31)) & 1u; }
+
+// Channels 8i..8i+7 of the lane's row, those outside the group zeroed, bf16 -> fp32.
+__device__ __forceinline__ void load_masked8(const uint16_t* xv, int i, const ChanMask& m, float* o) {
+    const uint4 w = reinterpret_cast<const uint4*>(xv)[i];
+    const uint32_t h[8] = {w.x & 0xFFFFu, w.x >> 16, w.y & 0xFFFFu, w.y >> 16,
+                           w.z & 0xFFFFu, w.z >> 16, w.w & 0xFFFFu, w.w >> 16};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = in_group(m, 8 * i + k) ? tq::bf16_to_f32(h[k]) : 0.0f;
+}
+
+__device__ __forceinline__ void load_masked(const uint16_t* xv, const ChanMask& m, float* o) {
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) load_masked8(xv, i, m, o + 8 * i);
+}
+
+// #{i : b[i] < z} (torch.bucketize right=False) by binary search over the sorted
+// boundaries in LDS: the predicate holds on a prefix, `bits` probes.
+__device__ __forceinline__ uint32_t bucket_lds(float z, const float* s_b, int bits) {
+    uint32_t c = 0;
+    for (uint32_t s = 1u << (bits - 1); s > 0; s >>= 1) c += (s_b[c + s - 1] < z) ? s : 0u;
+    return c;
+}
+
+// LSB-first bit stream written byte by byte into the lane's own row.
+struct ByteWriter {
+    uint8_t* dst;
+    uint32_t acc = 0;
+    int fill = 0;
+    __device__ __forceinline__ explicit ByteWriter(uint8_t* d) : dst(d) {}
+    __device__ __forceinline__ void put(uint32_t v, int nbits) {  // nbits <= 8: at most one byte
+        acc |= v << fill;
+        fill += nbits;
+        if (fill >= 8) {
+            *dst++ = (uint8_t)acc;
+            acc >>= 8;
+            fill -= 8;
+        }
+    }
+    __device__ __forceinline__ void flush() {
+        if (fill > 0) *dst = (uint8_t)acc;
+    }
+};
+
+template <bool PROD>
+__global__ __launch_bounds__(GBLOCK) void quantize_group_kernel(
+    const uint16_t* __restrict__ x, int heads, int64_t tokens, int64_t n_vec, int64_t x_sb, int64_t x_sh,
+    int64_t x_st, ChanMask mask, int sub_dim, int bits, const float* __restrict__ R,
+    const float* __restrict__ centers, const float* __restrict__ boundaries, const float* __restrict__ S,
+    uint8_t* __restrict__ codes, uint16_t* __restrict__ norms, uint8_t* __restrict__ signs,
+    uint16_t* __restrict__ rnorms, int64_t out_cap, int64_t out_offset) {
+    __shared__ float s_bound[(1 << MAX_BITS) - 1];
+    __shared__ float s_centers[PROD ? (1 << MAX_BITS) : 1];
+    __shared__ uint8_t s_code[PROD ? D : 1][GBLOCK];  // PROD: codes of each lane, column per lane
+    const int nb = (1 << bits) - 1;
+    for (int i = threadIdx.x; i < nb; i += GBLOCK) s_bound[i] = boundaries[i];
+    if (PROD)
+        for (int i = threadIdx.x; i <= nb; i += GBLOCK) s_centers[i] = centers[i];
+    __syncthreads();
+
+    const int64_t v = (int64_t)blockIdx.x * GBLOCK + threadIdx.x;
+    if (v >= n_vec) return;  // no barrier below this point
+    const int64_t t = v % tokens;
+    const int64_t gh = v / tokens;
+    const int64_t h = gh % heads;
+    const int64_t b = gh / heads;
+    const uint16_t* xv = x + b * x_sb + h * x_sh + t * x_st;
+    const int64_t slot = gh * out_cap + out_offset + t;
+
+    // ---- norm and direction of the group's sub-vector
+    float u[D];
+    load_masked(xv, mask, u);
+    float ss = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) ss = __builtin_fmaf(u[d], u[d], ss);
+    float n = tq::sqrt_rn(ss);
+    if (!(n > 0.0f)) n = 1.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) u[d] = tq::div_rn(u[d], n);
+    const uint32_t n16 = tq::f32_to_f16(n);
+    norms[slot] = (uint16_t)n16;
+
+    // ---- rotate (rows j < d), bucketize, pack
+    ByteWriter bw(codes + slot * (int64_t)((sub_dim * bits + 7) >> 3));
+    for (int j = 0; j < sub_dim; ++j) {
+        const float* rj = R + j * D;
+        float z = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) z = __builtin_fmaf(u[d], rj[d], z);
+        const uint32_t c = bucket_lds(z, s_bound, bits);
+        bw.put(c, bits);
+        if (PROD) s_code[j][threadIdx.x] = (uint8_t)c;
+    }
+    bw.flush();
+
+    if constexpr (PROD) {
+        // ---- residual decode khat = bf16((C[code] @ R) * f32(f16(n))), rows j < d
+        float* acc = u;  // u is dead after the rotation
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        for (int j = 0; j < sub_dim; ++j) {
+            const float cj = s_centers[s_code[j][threadIdx.x]];
+            const float* rj = R + j * D;
+#pragma unroll
+            for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
+        }
+        const float nf = tq::f16_to_f32(n16);
+        __asm__ volatile("" ::: "memory");  // x is re-read here, 16 bytes at a time, not held
+        float rs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < D / 8; ++i) {
+            float xr[8];
+            load_masked8(xv, i, mask, xr);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int d = 8 * i + k;
+                const float kh = tq::bf16_to_f32(tq::f32_to_bf16(acc[d] * nf));
+                acc[d] = xr[k] - kh;  // 0 - 0 outside the group: R's columns there are zero
+                rs = __builtin_fmaf(acc[d], acc[d], rs);
+            }
+        }
+        float rho = tq::sqrt_rn(rs);
+        if (!(rho > 0.0f)) rho = 1.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = tq::div_rn(acc[d], rho);
+        rnorms[slot] = (uint16_t)tq::f32_to_f16(rho);
+        ByteWriter sw(signs + slot * (int64_t)((sub_dim + 7) >> 3));
+        for (int i = 0; i < sub_dim; ++i) {
+            const float* si = S + i * D;
+            float p = 0.0f;
+#pragma unroll
+            for (int d = 0; d < D; ++d) p = __builtin_fmaf(acc[d], si[d], p);
+            sw.put(p >= 0.0f ? 1u : 0u, 1);
+        }
+        sw.flush();
+    }
+}
+
+// out = bf16((C[code] @ R) * f32(norm)) on the group's channels; with QJL (Q_prod keys)
+// corr = bf16(((s @ S) * rnorm) * qs), out = bf16(f32(khat) + f32(corr)).  Channels
+// outside the group are zeroed, or kept from `out` when `merge` is set.
+template <bool QJL>
+__global__ __launch_bounds__(GBLOCK) void dequantize_group_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms, const uint8_t* __restrict__ signs,
+    const uint16_t* __restrict__ rnorms, int64_t tokens, int64_t cap, int64_t n_vec, ChanMask mask, int sub_dim,
+    int bits, const float* __restrict__ R, const float* __restrict__ centers, const float* __restrict__ S, float qs,
+    int merge, uint16_t* __restrict__ out) {
+    __shared__ float s_centers[1 << MAX_BITS];
+    for (int i = threadIdx.x; i < (1 << bits); i += GBLOCK) s_centers[i] = centers[i];
+    __syncthreads();
+    const int64_t v = (int64_t)blockIdx.x * GBLOCK + threadIdx.x;
+    if (v >= n_vec) return;
+    const int64_t g = v / tokens, t = v % tokens;
+    const int64_t slot = g * cap + t;
+    const uint8_t* row = codes + slot * (int64_t)((sub_dim * bits + 7) >> 3);
+    const uint32_t cmask = (1u << bits) - 1u;
+    float acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+    for (int j = 0; j < sub_dim; ++j) {
+        const int pos = j * bits;
+        uint32_t pair = row[pos >> 3];
+        if ((pos & 7) + bits > 8) pair |= (uint32_t)row[(pos >> 3) + 1] << 8;
+        const float cj = s_centers[(pair >> (pos & 7)) & cmask];
+        const float* rj = R + j * D;
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
+    }
+    const float nf = tq::f16_to_f32(norms[slot]);
+    uint32_t kh[D / 2];  // bf16 pairs
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i)
+        kh[i] = tq::f32_to_bf16(acc[2 * i] * nf) | (tq::f32_to_bf16(acc[2 * i + 1] * nf) << 16);
+    if constexpr (QJL) {
+        const uint8_t* srow = signs + slot * (int64_t)((sub_dim + 7) >> 3);
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+        for (int i = 0; i < sub_dim; ++i) {
+            const float si = ((srow[i >> 3] >> (i & 7)) & 1u) ? 1.0f : -1.0f;
+            const float* Si = S + i * D;
+#pragma unroll
+            for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(si, Si[d], acc[d]);
+        }
+        const float rn = tq::f16_to_f32(rnorms[slot]);
+#pragma unroll
+        for (int i = 0; i < D / 2; ++i) {
+            const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((acc[2 * i] * rn) * qs));
+            const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((acc[2 * i + 1] * rn) * qs));
+            const float k0 = tq::bf16_to_f32(kh[i] & 0xFFFFu) + c0;
+            const float k1 = tq::bf16_to_f32(kh[i] >> 16) + c1;
+            kh[i] = tq::f32_to_bf16(k0) | (tq::f32_to_bf16(k1) << 16);
+        }
+    }
+    uint4* o4 = reinterpret_cast<uint4*>(out + v * D);
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+        uint32_t m[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            m[k] = (in_group(mask, 8 * i + 2 * k) ? 0x0000FFFFu : 0u) |
+                   (in_group(mask, 8 * i + 2 * k + 1) ? 0xFFFF0000u : 0u);
+        uint4 w = make_uint4(kh[4 * i] & m[0], kh[4 * i + 1] & m[1], kh[4 * i + 2] & m[2], kh[4 * i + 3] & m[3]);
+        if (merge) {
+            const uint4 old = o4[i];
+            w.x |= old.x & ~m[0];
+            w.y |= old.y & ~m[1];
+            w.z |= old.z & ~m[2];
+            w.w |= old.w & ~m[3];
+        }
+        o4[i] = w;
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Validates a group's channel list (host memory): 1 <= sub_dim <= dim, strictly
+// ascending, within [0, dim).  dim must be the kernels' D.
+int group_mask(const int32_t* channels, int sub_dim, int dim, ChanMask* m) {
+    if (!channels || sub_dim < 1 || dim < 1 || sub_dim > dim) return TQ_ERR_INVALID_ARGUMENT;
+    if (dim != D) return TQ_ERR_UNSUPPORTED;
+    for (int k = 0; k < D / 32; ++k) m->w[k] = 0;
+    for (int i = 0; i < sub_dim; ++i) {
+        const int32_t c = channels[i];
+        if (c < 0 || c >= dim || (i > 0 && c <= channels[i - 1])) return TQ_ERR_INVALID_ARGUMENT;
+        m->w[c >> 5] |= 1u << (c & 31);
+    }
+    return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" int tq_group_matrix(const float* sub, int sub_dim, const int32_t* channels, int dim, float* out) {
+    if (!sub || !out || !channels || sub_dim < 1 || dim < 1 || sub_dim > dim) return TQ_ERR_INVALID_ARGUMENT;
+    for (int i = 0; i < sub_dim; ++i)
+        if (channels[i] < 0 || channels[i] >= dim || (i > 0 && channels[i] <= channels[i - 1]))
+            return TQ_ERR_INVALID_ARGUMENT;
+    for (int64_t k = 0; k < (int64_t)dim * dim; ++k) out[k] = 0.0f;
+    for (int j = 0; j < sub_dim; ++j)
+        for (int i = 0; i < sub_dim; ++i) out[(int64_t)j * dim + channels[i]] = sub[(int64_t)j * sub_dim + i];
+    return TQ_OK;
+}
+
+extern "C" int tq_quantize_group(const uint16_t* x, int batch, int heads, int64_t tokens, int dim, int64_t x_sb,
+                                 int64_t x_sh, int64_t x_st, const int32_t* channels, int sub_dim, int bits,
+                                 const float* rotation, const float* centers, const float* boundaries,
+                                 const float* qjl, uint8_t* codes, uint16_t* norms, uint8_t* signs,
+                                 uint16_t* rnorms, int64_t out_cap, int64_t out_offset, void* stream) {
+    if (!x || batch < 0 || heads < 0 || tokens < 0 || out_offset < 0 || out_offset + tokens > out_cap)
+        return TQ_ERR_INVALID_ARGUMENT;
+    ChanMask mask;
+    int st = group_mask(channels, sub_dim, dim, &mask);
+    if (st != TQ_OK) return st;
+    if (bits < 1 || bits > MAX_BITS) return TQ_ERR_INVALID_ARGUMENT;
+    const bool prod = qjl != nullptr;
+    if (!rotation || !boundaries || !codes || !norms) return TQ_ERR_INVALID_ARGUMENT;
+    if (prod && (!centers || !signs || !rnorms)) return TQ_ERR_INVALID_ARGUMENT;
+    if (!aligned16(x) || (x_sb % 8) || (x_sh % 8) || (x_st % 8)) return TQ_ERR_UNSUPPORTED;
+    const int64_t n_vec = (int64_t)batch * heads * tokens;
+    const int64_t blocks = (n_vec + GBLOCK - 1) / GBLOCK;
+    if (blocks == 0) return TQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (prod)
+        hipLaunchKernelGGL((quantize_group_kernel<true>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, x, heads,
+                           tokens, n_vec, x_sb, x_sh, x_st, mask, sub_dim, bits, rotation, centers, boundaries, qjl,
+                           codes, norms, signs, rnorms, out_cap, out_offset);
+    else
+        hipLaunchKernelGGL((quantize_group_kernel<false>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, x, heads,
+                           tokens, n_vec, x_sb, x_sh, x_st, mask, sub_dim, bits, rotation, nullptr, boundaries,
+                           nullptr, codes, norms, nullptr, nullptr, out_cap, out_offset);
+    TQ_CHECK_LAUNCH();
+    return TQ_OK;
+}
+
+extern "C" int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
+                                   const uint16_t* rnorms, int64_t groups, int64_t tokens, int64_t cap, int dim,
+                                   const int32_t* channels, int sub_dim, int bits, const float* rotation,
+                                   const float* centers, const float* qjl, int merge, uint16_t* out,
+                                   void* stream) {
+    if (!codes || !norms || !rotation || !centers || !out || groups < 0 || tokens < 0 || tokens > cap)
+        return TQ_ERR_INVALID_ARGUMENT;
+    ChanMask mask;
+    int st = group_mask(channels, sub_dim, dim, &mask);
+    if (st != TQ_OK) return st;
+    if (bits < 1 || bits > MAX_BITS) return TQ_ERR_INVALID_ARGUMENT;
+    const bool has_qjl = qjl != nullptr;
+    if (has_qjl && (!signs || !rnorms)) return TQ_ERR_INVALID_ARGUMENT;
+    if (!aligned16(out)) return TQ_ERR_UNSUPPORTED;
+    const int64_t n_vec = groups * tokens;
+    const int64_t blocks = (n_vec + GBLOCK - 1) / GBLOCK;
+    if (blocks == 0) return TQ_OK;
+    // sqrt(pi/2)/d in double, rounded once to fp32 (the reference multiplies an fp32
+    // tensor by this Python float)
+    const float qs = (float)(sqrt(M_PI / 2.0) / (double)sub_dim);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (has_qjl)
+        hipLaunchKernelGGL((dequantize_group_kernel<true>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, codes, norms,
+                           signs, rnorms, tokens, cap, n_vec, mask, sub_dim, bits, rotation, centers, qjl, qs,
+                           merge != 0, out);
+    else
+        hipLaunchKernelGGL((dequantize_group_kernel<false>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, codes,
+                           norms, nullptr, nullptr, tokens, cap, n_vec, mask, sub_dim, bits, rotation, centers,
+                           nullptr, qs, merge != 0, out);
+    TQ_CHECK_LAUNCH();
+    return TQ_OK;
+}

@@ -226,16 +226,16 @@ def activate(model, tokenizer=None, *, bits: int = 4, rotation_seed: int = 0, nu
              norm_guard: bool = True, quiet: bool = False) -> None:
     """Activate TurboQuant on an existing HuggingFace model (reference :329-450).
 
-    Raises RuntimeError if already active, ValueError if the model is incompatible
-    or no tokenizer can be found, NotImplementedError for the outlier split.
+    Raises RuntimeError if already active, ValueError if the model is incompatible,
+    a bit width is out of range or no tokenizer can be found.
     """
     if hasattr(model, "_tq_state"):
         raise RuntimeError("TurboQuant is already active on this model. Call turboquant.deactivate(model) first.")
     report = inspect_transformers_model_compatibility(model)
     if not report.compatible:
         raise ValueError(f"Model is not compatible with TurboQuant: {report.reasons}")
-    if num_outlier_channels:
-        raise NotImplementedError("num_outlier_channels > 0 (outlier split) is not supported by the MI355X path")
+    if num_outlier_channels and not 1 <= bits + outlier_extra_bits <= 8:
+        raise ValueError(f"outlier bits {bits}+{outlier_extra_bits} out of range (the channel-group kernels pack 1-8)")
     if bits not in (1, 2, 3, 4) or (use_qjl_keys and bits < 2):
         raise ValueError(f"bits={bits} unsupported (Q_mse: 1-4, Q_prod: 2-4)")
     if tokenizer is None:

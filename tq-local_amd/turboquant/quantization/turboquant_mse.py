@@ -24,9 +24,10 @@ import numpy as np
 import torch
 
 #: seed offsets of the reference's seed schedule
-#: (``runtime/packed_qmse_cache.py:117-118, 262, 278``)
+#: (``runtime/packed_qmse_cache.py:117-118, 255, 262, 265, 278``)
 KEY_ROTATION_SEED_OFFSET = 1
 QJL_SEED_OFFSET = 31337
+OUTLIER_SEED_OFFSET = 7919
 
 DEFAULT_GRID_SIZE = 32769
 

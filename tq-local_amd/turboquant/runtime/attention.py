@@ -10,6 +10,12 @@ layers) it is plain SDPA, as in the reference.
 (``runtime/triton_kernels.py:238-368``).  Unlike the reference it accepts any
 batch size (one query token per row) and honours left/right padding from the
 attention mask; it has no fallback path -- shapes it does not cover raise.
+
+Outlier-split layers take ``split_attention``: the reference's fused kernel
+refuses them (``triton_kernels.py:252-253``) and its chunked path
+(``runtime/attention.py:215-304``) decodes K and V to bf16 and runs exact
+softmax attention; here libtq's channel-group kernels do the decoding and the
+softmax runs in fp32 on the device.
 """
 
 from __future__ import annotations
@@ -57,8 +63,12 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
     """Decode attention of [B, Hq, 1, D] queries over a packed layer -> [B, Hq, 1, D].
 
     The logit scale is 1/sqrt(D) (reference ``triton_kernels.py:285``).  Tokens
-    kept dense (``quantize_decode=False``) are merged by log-sum-exp.
+    kept dense (``quantize_decode=False``) are merged by log-sum-exp.  An
+    outlier-split layer is handed to ``split_attention`` (where the reference
+    returns None and its caller takes the chunked path).
     """
+    if packed_layer._outlier_enabled:
+        return split_attention(query_states, packed_layer, n_kv_groups, attention_mask)
     B, Hq, Sq, D = query_states.shape
     if Sq != 1:
         raise NotImplementedError("TurboQuant fused attention takes one decode token per sequence "
@@ -93,6 +103,37 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
     num = o_packed * wp[..., None] + (wd[..., None] * dv).sum(dim=2)
     den = (wp + wd.sum(dim=-1)).clamp(min=1e-30)[..., None]
     return (num / den).to(query_states.dtype).view(B, Hq, 1, D)
+
+
+def split_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", n_kv_groups: int,
+                    attention_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of [B, Hq, 1, D] queries over an outlier-split layer -> [B, Hq, 1, D].
+
+    K^ and V^ are the bf16 rows of both channel groups decoded by libtq (reference
+    ``_decode_keys_range`` / ``_decode_values_range``, runtime/packed_qmse_cache.py:564-592),
+    followed by the dense decode buffer; logits are fp32 ``q . K^ / sqrt(D)``, the
+    softmax is exact and the normaliser is clamped at 1e-8 (runtime/attention.py:189-304).
+    """
+    B, Hq, Sq, D = query_states.shape
+    if Sq != 1:
+        raise NotImplementedError(f"TurboQuant decode attention takes one token per sequence (got {Sq})")
+    keys, values = packed_layer._decode_keys_full(), packed_layer._decode_values_full()
+    if packed_layer._dense_keys is not None:
+        keys = torch.cat((keys, packed_layer._dense_keys.to(keys.dtype)), dim=-2)
+        values = torch.cat((values, packed_layer._dense_values.to(values.dtype)), dim=-2)
+    Hkv, N = keys.shape[1], keys.shape[2]
+    q = query_states.float().reshape(B, Hkv, n_kv_groups, D)  # query head h reads KV head h // groups
+    logits = torch.matmul(q, keys.float().transpose(-2, -1)) * (1.0 / math.sqrt(D))  # [B, Hkv, G, N]
+    starts, ends = _valid_range(attention_mask, B, N, query_states.device)
+    if starts is not None:
+        pos = torch.arange(N, device=logits.device)
+        ok = (pos[None, :] >= starts[:, None]) & (pos[None, :] < ends[:, None])
+        logits = logits.masked_fill(~ok[:, None, None, :], float("-inf"))
+    m = logits.amax(dim=-1, keepdim=True)
+    m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+    p = torch.exp(logits - m)
+    out = torch.matmul(p, values.float()) / p.sum(dim=-1, keepdim=True).clamp(min=1e-8)
+    return out.reshape(B, Hq, 1, D).to(query_states.dtype)
 
 
 def _sdpa_fallback(module, query, key, value, attention_mask, scaling):

@@ -9,6 +9,10 @@ Reference interfaces replaced:
   quantize_prod  -> PackedMSELayer._encode_keys_qjl_group  runtime/packed_qmse_cache.py:285-310
   dequantize_mse -> PackedMSELayer._decode_group           runtime/packed_qmse_cache.py:404-435
   decode_attention -> fused_attention                      runtime/triton_kernels.py:238-368
+  quantize_group -> PackedMSELayer._encode_split / _encode_keys_split_qjl (one channel group)
+                                                           runtime/packed_qmse_cache.py:481-496, 437-454
+  dequantize_group -> PackedMSELayer._decode_merge / _decode_keys_merge_qjl (one channel group)
+                                                           runtime/packed_qmse_cache.py:498-515, 456-479
 """
 
 from __future__ import annotations
@@ -17,6 +21,7 @@ import ctypes
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from turboquant.runtime import _lib
@@ -52,6 +57,41 @@ class CodecParams:
     rotation: torch.Tensor  # fp32 [D, D]
     centers: torch.Tensor  # fp32 [2^bits]
     boundaries: torch.Tensor  # fp32 [2^bits - 1]
+
+
+@dataclass
+class GroupCodec:
+    """Device-resident codec of one channel group (the outlier-channel split).
+
+    ``rotation`` / ``qjl`` are the group's own d x d matrices (the reference's
+    attributes); ``rotation_ch`` / ``qjl_ch`` are the same matrices in channel
+    space (``group_matrix``), which is what libtq takes.  ``qjl`` is set only for
+    Q_prod key groups.
+    """
+
+    channels: np.ndarray  # int32 [d], host, strictly ascending
+    bits: int
+    rotation: torch.Tensor  # fp32 [d, d]
+    centers: torch.Tensor  # fp32 [2^bits]
+    boundaries: torch.Tensor  # fp32 [2^bits - 1]
+    rotation_ch: torch.Tensor  # fp32 [D, D]
+    qjl: torch.Tensor | None = None  # fp32 [d, d]
+    qjl_ch: torch.Tensor | None = None  # fp32 [D, D]
+
+    @property
+    def dim(self) -> int:
+        return int(self.channels.shape[0])
+
+
+def group_matrix(sub: np.ndarray, channels: np.ndarray, dim: int = HEAD_DIM) -> np.ndarray:
+    """Channel-space form of a group's d x d matrix (host): out[j, channels[i]] = sub[j, i]."""
+    sub = np.ascontiguousarray(sub, dtype=np.float32)
+    ch = np.ascontiguousarray(channels, dtype=np.int32)
+    if sub.shape != (ch.size, ch.size):
+        raise ValueError(f"group matrix {sub.shape} does not match {ch.size} channels")
+    out = np.empty((dim, dim), np.float32)
+    _lib.call("tq_group_matrix", sub.ctypes.data, ch.size, ch.ctypes.data, dim, out.ctypes.data)
+    return out
 
 
 def _as_encoder_input(x: torch.Tensor) -> torch.Tensor:
@@ -97,6 +137,49 @@ def quantize_prod(x: torch.Tensor, codec: CodecParams, qjl: torch.Tensor, codes:
     _lib.call("tq_quantize_prod", _vp(x), B, H, T, D, x.stride(0), x.stride(1), x.stride(2), codec.bits,
               _vp(codec.rotation), _vp(codec.centers), _vp(codec.boundaries), _vp(qjl), _vp(codes), _vp(norms),
               _vp(signs), _vp(rnorms), cap, offset, _stream(x.device))
+
+
+def quantize_group(x: torch.Tensor, g: GroupCodec, codes: torch.Tensor, norms: torch.Tensor,
+                   signs: torch.Tensor | None = None, rnorms: torch.Tensor | None = None, offset: int = 0) -> None:
+    """Encode channel group ``g`` of x [B,H,T,D] at token slot ``offset``: Q_mse codes,
+    plus the QJL sketch when ``g`` is a Q_prod key group (``signs`` / ``rnorms`` then required).
+    codes [B,H,cap,ceil(d*bits/8)], norms / rnorms [B,H,cap], signs [B,H,cap,ceil(d/8)]."""
+    x = _as_encoder_input(x)
+    prod = g.qjl_ch is not None
+    _require_gpu(x, codes, norms, signs, rnorms, g.rotation_ch)
+    B, H, T, D = x.shape
+    cap = codes.shape[2]
+    if codes.shape != (B, H, cap, row_bytes(g.dim, g.bits)) or codes.dtype != torch.uint8 or not codes.is_contiguous():
+        raise ValueError(f"codes buffer {tuple(codes.shape)} does not match group ({g.dim} channels, {g.bits} bits)")
+    if prod:
+        if signs is None or rnorms is None:
+            raise ValueError("a Q_prod key group needs signs and rnorms buffers")
+        if signs.shape != (B, H, cap, row_bytes(g.dim, 1)) or not signs.is_contiguous():
+            raise ValueError("signs buffer shape mismatch")
+    for t in (norms, rnorms if prod else None):
+        if t is not None and (t.shape != (B, H, cap) or t.dtype != torch.float16 or not t.is_contiguous()):
+            raise ValueError("norm buffers must be contiguous float16 [B, H, cap]")
+    _lib.call("tq_quantize_group", _vp(x), B, H, T, D, x.stride(0), x.stride(1), x.stride(2), g.channels.ctypes.data,
+              g.dim, g.bits, _vp(g.rotation_ch), _vp(g.centers), _vp(g.boundaries), _vp(g.qjl_ch), _vp(codes),
+              _vp(norms), _vp(signs if prod else None), _vp(rnorms if prod else None), cap, offset, _stream(x.device))
+
+
+def dequantize_group(codes: torch.Tensor, norms: torch.Tensor, tokens: int, g: GroupCodec, out: torch.Tensor,
+                     merge: bool, signs: torch.Tensor | None = None, rnorms: torch.Tensor | None = None) -> None:
+    """Decode channel group ``g`` of codes [B,H,cap,row] into out bf16 [B,H,tokens,D] (its
+    channels; the others are zeroed, or kept when ``merge``).  QJL-corrected when ``g``
+    is a Q_prod key group."""
+    _require_gpu(codes, norms, out, signs, rnorms)
+    B, H, cap, _ = codes.shape
+    qjl = g.qjl_ch is not None
+    if qjl and (signs is None or rnorms is None):
+        raise ValueError("a Q_prod key group needs its signs and rnorms")
+    if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.shape[:3] != (B, H, tokens):
+        raise ValueError("out must be a contiguous bf16 [B, H, tokens, D] tensor")
+    _lib.call("tq_dequantize_group", _vp(codes), _vp(norms), _vp(signs if qjl else None),
+              _vp(rnorms if qjl else None), B * H, tokens, cap, out.shape[-1], g.channels.ctypes.data, g.dim,
+              g.bits, _vp(g.rotation_ch), _vp(g.centers), _vp(g.qjl_ch), int(bool(merge)), _vp(out),
+              _stream(codes.device))
 
 
 def dequantize_mse(codes: torch.Tensor, norms: torch.Tensor, tokens: int, codec: CodecParams,

@@ -14,8 +14,11 @@ Differences, all on purpose:
 * Every encode / decode is a libtq HIP kernel; there is no CPU path.
 * ``get_mask_sizes(query_length)`` / ``get_max_length()`` follow the installed
   transformers (5.x) cache-layer protocol.
-* The outlier-channel split (``num_outlier_channels > 0``) is not implemented:
-  it is off by default in the reference and its fused path refuses it.
+* The outlier-channel split (``num_outlier_channels > 0``, reference :95-114,
+  :437-535) encodes and decodes each channel group with libtq's channel-group
+  kernels, in prefill and in decode-append alike (the reference's lazy
+  decode-append ignores the split and hands the 128-channel token to the
+  normal group's smaller rotation).
 """
 
 from __future__ import annotations
@@ -29,7 +32,7 @@ import torch
 from transformers.cache_utils import Cache, CacheLayerMixin
 
 from turboquant.runtime import kernels as K
-from turboquant.runtime.params import LayerCodecs, layer_codecs
+from turboquant.runtime.params import LayerCodecs, SplitCodecs, layer_codecs, split_codecs
 
 #: growth step of the capacity buffers when decode-append runs out of slots
 DEFAULT_RESERVE_TOKENS = 256
@@ -72,31 +75,42 @@ class PackedQJL:
                    + self.residual_norms.numel() * self.residual_norms.element_size())
 
 
-class _Store:
-    """Capacity buffers of one packed layer; slots [0, length) are valid."""
+def detect_outlier_channels(key_states: torch.Tensor, value_states: torch.Tensor,
+                            num_outlier_channels: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(outlier, normal) channel indices, both ascending: the channels of largest
+    combined key + value energy (reference runtime/packed_qmse_cache.py:95-114)."""
+    combined = key_states.float().pow(2).sum(dim=(0, 1, 2)) + value_states.float().pow(2).sum(dim=(0, 1, 2))
+    outlier = torch.topk(combined, num_outlier_channels).indices.sort().values
+    keep = torch.ones(combined.shape[0], dtype=torch.bool, device=combined.device)
+    keep[outlier] = False
+    return outlier, torch.arange(combined.shape[0], device=combined.device)[keep]
 
-    def __init__(self, B: int, H: int, D: int, cap: int, codecs: LayerCodecs, device: torch.device):
-        self.B, self.H, self.D, self.codecs, self.device = B, H, D, codecs, device
+
+class _Store:
+    """Capacity buffers of one packed layer; slots [0, length) are valid.
+
+    ``spec`` maps each buffer name to (trailing row shape, dtype), or to None for a
+    buffer the layer does not have; buffers are [B, H, cap, *row] and are reachable
+    as attributes of the store (None when absent)."""
+
+    def __init__(self, B: int, H: int, cap: int, device: torch.device,
+                 spec: dict[str, tuple[tuple, torch.dtype] | None]):
+        self.B, self.H, self.device, self.spec = B, H, device, spec
         self.length = 0
         self.cap = 0
-        self.kc = self.kn = self.ks = self.kr = self.vc = self.vn = None
+        for name in spec:
+            setattr(self, name, None)
         self._alloc(cap)
 
     def _alloc(self, cap: int) -> None:
-        B, H, D, c = self.B, self.H, self.D, self.codecs
-        dev = self.device
-        new = {
-            "kc": torch.zeros(B, H, cap, K.row_bytes(D, c.key_bits), dtype=torch.uint8, device=dev),
-            "kn": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
-            "vc": torch.zeros(B, H, cap, K.row_bytes(D, c.value_bits), dtype=torch.uint8, device=dev),
-            "vn": torch.zeros(B, H, cap, dtype=torch.float16, device=dev),
-            "ks": torch.zeros(B, H, cap, D // 8, dtype=torch.uint8, device=dev) if c.use_qjl_keys else None,
-            "kr": torch.zeros(B, H, cap, dtype=torch.float16, device=dev) if c.use_qjl_keys else None,
-        }
         n = self.length
-        for name, buf in new.items():
+        for name, entry in self.spec.items():
+            if entry is None:
+                continue
+            row, dtype = entry
+            buf = torch.zeros(self.B, self.H, cap, *row, dtype=dtype, device=self.device)
             old = getattr(self, name)
-            if buf is not None and old is not None and n:
+            if old is not None and n:
                 buf[:, :, :n].copy_(old[:, :, :n])
             setattr(self, name, buf)
         self.cap = cap
@@ -106,16 +120,26 @@ class _Store:
         if need > self.cap:
             self._alloc(max(need + reserve_tokens, 2 * self.cap))
 
-    def append(self, k: torch.Tensor, v: torch.Tensor, reserve_tokens: int) -> None:
-        T = int(k.shape[2])
-        self.reserve(T, reserve_tokens)
-        c = self.codecs
-        if c.use_qjl_keys:
-            K.quantize_prod(k, c.key, c.qjl, self.kc, self.kn, self.ks, self.kr, offset=self.length)
-        else:
-            K.quantize_mse(k, c.key, self.kc, self.kn, offset=self.length)
-        K.quantize_mse(v, c.value, self.vc, self.vn, offset=self.length)
-        self.length += T
+
+def _flat_spec(D: int, c: LayerCodecs) -> dict[str, tuple[tuple, torch.dtype] | None]:
+    spec = {"kc": ((K.row_bytes(D, c.key_bits),), torch.uint8), "kn": ((), torch.float16),
+            "vc": ((K.row_bytes(D, c.value_bits),), torch.uint8), "vn": ((), torch.float16)}
+    qjl = c.use_qjl_keys
+    spec.update(ks=((K.row_bytes(D, 1),), torch.uint8) if qjl else None, kr=((), torch.float16) if qjl else None)
+    return spec
+
+
+def _split_spec(sc: SplitCodecs) -> dict[str, tuple[tuple, torch.dtype] | None]:
+    """Normal group: kc kn (ks kr) vc vn; outlier group: the same names with an 'o'."""
+    spec = {}
+    for sfx, kg, vg in (("", sc.key_normal, sc.value_normal), ("o", sc.key_outlier, sc.value_outlier)):
+        spec["kc" + sfx] = ((K.row_bytes(kg.dim, kg.bits),), torch.uint8)
+        spec["kn" + sfx] = ((), torch.float16)
+        spec["ks" + sfx] = ((K.row_bytes(kg.dim, 1),), torch.uint8) if sc.use_qjl_keys else None
+        spec["kr" + sfx] = ((), torch.float16) if sc.use_qjl_keys else None
+        spec["vc" + sfx] = ((K.row_bytes(vg.dim, vg.bits),), torch.uint8)
+        spec["vn" + sfx] = ((), torch.float16)
+    return spec
 
 
 class PackedMSELayer(CacheLayerMixin):
@@ -128,9 +152,6 @@ class PackedMSELayer(CacheLayerMixin):
                  outlier_extra_bits: int = 1, use_qjl_keys: bool = False, quantize_decode: bool = False,
                  reserve_tokens: int = DEFAULT_RESERVE_TOKENS):
         super().__init__()
-        if num_outlier_channels:
-            raise NotImplementedError("the outlier-channel split (num_outlier_channels > 0) is not supported "
-                                      "by the MI355X TurboQuant path")
         self.bits = bits
         self.seed = seed
         self.grid_size = grid_size
@@ -141,7 +162,8 @@ class PackedMSELayer(CacheLayerMixin):
         self.reserve_tokens = reserve_tokens
         self.device: torch.device | None = None
         self.dtype: torch.dtype | None = None
-        self.codecs: LayerCodecs | None = None
+        self.codecs: LayerCodecs | None = None  # unsplit layers
+        self._split: SplitCodecs | None = None  # outlier-split layers
         self._store: _Store | None = None
         self._shape: tuple[int, int, int] | None = None  # (B, H, D)
         self._force_dense = False
@@ -151,76 +173,163 @@ class PackedMSELayer(CacheLayerMixin):
 
     # ------------------------------------------------------------- parameters
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        """Reference :237-283.  With 0 < num_outlier_channels < D the channels are split by
+        the first K/V seen (the prefill) and every later token uses the same split."""
         self.dtype = key_states.dtype
         self.device = key_states.device
-        self.codecs = layer_codecs(int(key_states.shape[-1]), self.bits, self.seed, self.use_qjl_keys, self.device,
-                                   self.grid_size)
+        D = int(key_states.shape[-1])
+        if 0 < self.num_outlier_channels < D:
+            outlier, normal = detect_outlier_channels(key_states, value_states, self.num_outlier_channels)
+            self._split = split_codecs(normal.cpu().numpy(), outlier.cpu().numpy(), self.bits,
+                                       self.outlier_extra_bits, self.seed, self.use_qjl_keys, self.device,
+                                       self.grid_size)
+        else:
+            self.codecs = layer_codecs(D, self.bits, self.seed, self.use_qjl_keys, self.device, self.grid_size)
         self.is_initialized = True
 
-    # reference-compatible parameter attributes
+    # reference-compatible parameter attributes (the normal group's on split layers)
+    def _value_codec(self):
+        return self._split.value_normal if self._split is not None else (self.codecs and self.codecs.value)
+
+    def _key_codec(self):
+        return self._split.key_normal if self._split is not None else (self.codecs and self.codecs.key)
+
     @property
     def rotation(self):
-        return None if self.codecs is None else self.codecs.value.rotation
+        c = self._value_codec()
+        return None if c is None else c.rotation
 
     @property
     def centers(self):
-        return None if self.codecs is None else self.codecs.value.centers
+        c = self._value_codec()
+        return None if c is None else c.centers
 
     @property
     def boundaries(self):
-        return None if self.codecs is None else self.codecs.value.boundaries
+        c = self._value_codec()
+        return None if c is None else c.boundaries
 
     @property
     def _key_rotation(self):
-        return None if self.codecs is None else self.codecs.key.rotation
+        c = self._key_codec()
+        return None if c is None else c.rotation
 
     @property
     def _key_centers(self):
-        return None if self.codecs is None else self.codecs.key.centers
+        c = self._key_codec()
+        return None if c is None else c.centers
 
     @property
     def _key_boundaries(self):
-        return None if self.codecs is None else self.codecs.key.boundaries
+        c = self._key_codec()
+        return None if c is None else c.boundaries
 
     @property
     def _qjl_matrix(self):
+        if self._split is not None:
+            return self._split.key_normal.qjl
         return None if self.codecs is None else self.codecs.qjl
 
     @property
     def _outlier_enabled(self) -> bool:
-        return False
+        return self._split is not None
+
+    @property
+    def _outlier_indices(self):
+        return None if self._split is None else self._split.outlier_indices
+
+    @property
+    def _normal_indices(self):
+        return None if self._split is None else self._split.normal_indices
+
+    @property
+    def _outlier_rotation(self):
+        return None if self._split is None else self._split.value_outlier.rotation
+
+    @property
+    def _outlier_centers(self):
+        return None if self._split is None else self._split.value_outlier.centers
+
+    @property
+    def _outlier_boundaries(self):
+        return None if self._split is None else self._split.value_outlier.boundaries
+
+    @property
+    def _key_outlier_rotation(self):
+        return self._split.key_outlier.rotation if self._split is not None and self.use_qjl_keys else None
+
+    @property
+    def _key_outlier_centers(self):
+        return self._split.key_outlier.centers if self._split is not None and self.use_qjl_keys else None
+
+    @property
+    def _key_outlier_boundaries(self):
+        return self._split.key_outlier.boundaries if self._split is not None and self.use_qjl_keys else None
+
+    @property
+    def _qjl_outlier_matrix(self):
+        return None if self._split is None else self._split.key_outlier.qjl
 
     # ---------------------------------------------------------- packed views
     def packed_seq_length(self) -> int:
         return 0 if self._store is None else self._store.length
 
-    def _view_shape(self) -> tuple[int, int, int, int]:
-        B, H, D = self._shape
-        return (B, H, self.packed_seq_length(), D)
-
-    @property
-    def keys_packed(self) -> PackedTensorMSE | None:
+    def _packed(self, codes: str, norms: str, dim: int, bits: int) -> PackedTensorMSE | None:
         s = self._store
         if s is None:
             return None
         n = s.length
-        return PackedTensorMSE(s.kc[:, :, :n], s.kn[:, :, :n], self._view_shape(), self.dtype, self.codecs.key_bits)
+        B, H, _ = self._shape
+        return PackedTensorMSE(getattr(s, codes)[:, :, :n], getattr(s, norms)[:, :, :n], (B, H, n, dim), self.dtype,
+                               bits)
 
-    @property
-    def values_packed(self) -> PackedTensorMSE | None:
-        s = self._store
-        if s is None:
-            return None
-        n = s.length
-        return PackedTensorMSE(s.vc[:, :, :n], s.vn[:, :, :n], self._view_shape(), self.dtype, self.codecs.value_bits)
-
-    @property
-    def _keys_qjl(self) -> PackedQJL | None:
+    def _qjl(self, signs: str, rnorms: str, dim: int) -> PackedQJL | None:
         s = self._store
         if s is None or not self.use_qjl_keys:
             return None
         n = s.length
-        return PackedQJL(s.ks[:, :, :n], s.kr[:, :, :n], self._shape[2])
+        return PackedQJL(getattr(s, signs)[:, :, :n], getattr(s, rnorms)[:, :, :n], dim)
+
+    @property
+    def keys_packed(self) -> PackedTensorMSE | None:
+        if self._split is not None:
+            g = self._split.key_normal
+            return self._packed("kc", "kn", g.dim, g.bits)
+        return None if self._store is None else self._packed("kc", "kn", self._shape[2], self.codecs.key_bits)
+
+    @property
+    def values_packed(self) -> PackedTensorMSE | None:
+        if self._split is not None:
+            g = self._split.value_normal
+            return self._packed("vc", "vn", g.dim, g.bits)
+        return None if self._store is None else self._packed("vc", "vn", self._shape[2], self.codecs.value_bits)
+
+    @property
+    def _keys_qjl(self) -> PackedQJL | None:
+        if self._store is None:
+            return None
+        dim = self._split.key_normal.dim if self._split is not None else self._shape[2]
+        return self._qjl("ks", "kr", dim)
+
+    @property
+    def _keys_outlier(self) -> PackedTensorMSE | None:
+        if self._split is None:
+            return None
+        g = self._split.key_outlier
+        return self._packed("kco", "kno", g.dim, g.bits)
+
+    @property
+    def _values_outlier(self) -> PackedTensorMSE | None:
+        if self._split is None:
+            return None
+        g = self._split.value_outlier
+        return self._packed("vco", "vno", g.dim, g.bits)
+
+    @property
+    def _keys_outlier_qjl(self) -> PackedQJL | None:
+        if self._split is None:
+            return None
+        return self._qjl("kso", "kro", self._split.key_outlier.dim)
 
     # ------------------------------------------------------------- encoding
     def initialize_from_dense(self, key_states: torch.Tensor, value_states: torch.Tensor, *,
@@ -237,20 +346,54 @@ class PackedMSELayer(CacheLayerMixin):
         self._append_packed(key_states, value_states)
 
     def _append_packed(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        B, H, T, D = key_states.shape
+        """Encode [B, H, T, D] keys / values into slots [N, N + T) of the capacity buffers."""
+        B, H, T, D = (int(v) for v in key_states.shape)
         if self._store is None:
-            self._shape = (int(B), int(H), int(D))
-            self._store = _Store(int(B), int(H), int(D), max(int(T) + self.reserve_tokens, 1), self.codecs,
-                                 key_states.device)
-        elif (int(B), int(H), int(D)) != self._shape:
+            self._shape = (B, H, D)
+            spec = _split_spec(self._split) if self._split is not None else _flat_spec(D, self.codecs)
+            self._store = _Store(B, H, max(T + self.reserve_tokens, 1), key_states.device, spec)
+        elif (B, H, D) != self._shape:
             raise ValueError(f"append of shape {tuple(key_states.shape)} to a cache of {self._shape}")
-        self._store.append(key_states, value_states, self.reserve_tokens)
+        s = self._store
+        s.reserve(T, self.reserve_tokens)
+        off = s.length
+        if self._split is not None:
+            sc = self._split
+            qjl = sc.use_qjl_keys
+            for sfx, kg, vg in (("", sc.key_normal, sc.value_normal), ("o", sc.key_outlier, sc.value_outlier)):
+                K.quantize_group(key_states, kg, getattr(s, "kc" + sfx), getattr(s, "kn" + sfx),
+                                 getattr(s, "ks" + sfx) if qjl else None, getattr(s, "kr" + sfx) if qjl else None,
+                                 offset=off)
+                K.quantize_group(value_states, vg, getattr(s, "vc" + sfx), getattr(s, "vn" + sfx), offset=off)
+        else:
+            c = self.codecs
+            if c.use_qjl_keys:
+                K.quantize_prod(key_states, c.key, c.qjl, s.kc, s.kn, s.ks, s.kr, offset=off)
+            else:
+                K.quantize_mse(key_states, c.key, s.kc, s.kn, offset=off)
+            K.quantize_mse(value_states, c.value, s.vc, s.vn, offset=off)
+        s.length += T
 
     # ------------------------------------------------------------- decoding
+    def _decode_split(self, pre: str, normal, outlier) -> torch.Tensor:
+        """Both channel groups decoded into one [B, H, N, D] bf16 tensor (reference
+        _decode_merge / _decode_keys_merge_qjl, :456-515)."""
+        s = self._store
+        B, H, D = self._shape
+        out = torch.empty(B, H, s.length, D, dtype=torch.bfloat16, device=s.device)
+        qjl = pre == "k" and self.use_qjl_keys
+        for sfx, g, merge in (("", normal, False), ("o", outlier, True)):
+            K.dequantize_group(getattr(s, pre + "c" + sfx), getattr(s, pre + "n" + sfx), s.length, g, out, merge,
+                               signs=getattr(s, "ks" + sfx) if qjl else None,
+                               rnorms=getattr(s, "kr" + sfx) if qjl else None)
+        return out
+
     def _decode_keys_full(self) -> torch.Tensor | None:
         s = self._store
         if s is None:
             return None
+        if self._split is not None:
+            return self._decode_split("k", self._split.key_normal, self._split.key_outlier).to(self.dtype)
         c = self.codecs
         if c.use_qjl_keys:
             return K.dequantize_prod(s.kc, s.kn, s.ks, s.kr, s.length, c.key, c.qjl).to(self.dtype)
@@ -260,6 +403,8 @@ class PackedMSELayer(CacheLayerMixin):
         s = self._store
         if s is None:
             return None
+        if self._split is not None:
+            return self._decode_split("v", self._split.value_normal, self._split.value_outlier).to(self.dtype)
         return K.dequantize_mse(s.vc, s.vn, s.length, self.codecs.value).to(self.dtype)
 
     # ------------------------------------------------------------ HF protocol
@@ -322,7 +467,8 @@ class PackedMSELayer(CacheLayerMixin):
     def storage_bytes(self) -> int:
         """Logical storage (N valid tokens, as the reference counts it; :874-885)."""
         total = 0
-        for p in (self.keys_packed, self.values_packed, self._keys_qjl):
+        for p in (self.keys_packed, self.values_packed, self._keys_qjl, self._keys_outlier, self._values_outlier,
+                  self._keys_outlier_qjl):
             if p is not None:
                 total += p.storage_bytes()
         for d in (self._dense_keys, self._dense_values):
