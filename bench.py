@@ -122,6 +122,85 @@ def cpu_baseline(bits: int = 4) -> dict:
     }
 
 
+def bench_split(args, dev) -> dict:
+    """Outlier-split layers (num_outlier_channels = --outliers): prefill through the
+    channel-group encoders (tq_quantize_group), then decode steps through the channel-group
+    attention kernel (tq_decode_attention_groups).  Launches are eager."""
+    import torch
+
+    from turboquant.runtime.attention import fused_attention
+    from turboquant.runtime.packed_qmse_cache import PackedMSELayer
+    from turboquant.runtime.synthetic import kv_bf16, query_bf16
+
+    B, Hq, Hkv, N, D, bits = args.batch, args.q_heads, args.kv_heads, args.context, 128, args.bits
+    qjl = not args.no_qjl
+    layers, queries, q_ms = [], [], []
+    for li in range(args.layers):
+        k = kv_bf16((B, Hkv, N, D), seed=1000 + 2 * li, device=dev, outlier_channels=args.outliers)
+        v = kv_bf16((B, Hkv, N, D), seed=1001 + 2 * li, device=dev)
+        layer = PackedMSELayer(bits=bits, num_outlier_channels=args.outliers, use_qjl_keys=qjl, quantize_decode=True,
+                               reserve_tokens=0)
+        layer.lazy_initialization(k, v)  # channel detection and codecs, outside the timed encode
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        layer.initialize_from_dense(k, v)
+        e1.record()
+        torch.cuda.synchronize()
+        q_ms.append(e0.elapsed_time(e1))
+        del k, v
+        layers.append(layer)
+        queries.append(query_bf16(B, Hq, D, seed=5000 + li, device=dev).unsqueeze(2))
+    print(f"[bench] split-quantized {args.layers} layers: {statistics.median(q_ms):.3f} ms/layer (median)",
+          file=sys.stderr, flush=True)
+
+    def attn(li):
+        return fused_attention(queries[li], layers[li], Hq // Hkv)
+
+    for _ in range(args.warmup):
+        for li in range(args.layers):
+            attn(li)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        for li in range(args.layers):
+            attn(li)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    avg_us = e0.elapsed_time(e1) * 1e3 / (args.steps * args.layers)
+    layer_bytes = int(layers[0].storage_bytes())
+    achieved = layer_bytes / (avg_us * 1e-6) / 1e9
+    return {
+        "metric": "outlier-split decode-attn us/layer (channel-group kernel), 8B KV shape @32K",
+        "value": round(avg_us, 1),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codes; fp32 VALU",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"outlier split, {args.outliers} channels: {args.layers} layers, B={B}, Hq={Hq}, Hkv={Hkv}, "
+                         f"D={D}, N={N}, {bits}-bit normal / {bits + 1}-bit outlier group, "
+                         + ("Q_prod keys" if qjl else "Q_mse keys")),
+            "packed_bytes_per_layer": layer_bytes,
+            "layers": args.layers,
+        },
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "tq_decode_attention_groups = group_attn_kernel + merge_kernel, eager calls"},
+        "prefill_quantizer": {"ms_per_layer": round(statistics.median(q_ms), 3)},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,6 +218,8 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed region, run a plain elementwise copy of one layer's packed size "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--outliers", type=int, default=0,
+                    help="measure outlier-split layers with this many outlier channels instead of the C2 line")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -157,6 +238,9 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.outliers:
+        print(json.dumps(bench_split(args, dev)))
+        return 0
     B, Hq, Hkv, N, D, bits = args.batch, args.q_heads, args.kv_heads, args.context, 128, args.bits
     qjl = not args.no_qjl
     lc = layer_codecs(D, bits, 0, qjl, dev)

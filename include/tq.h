@@ -181,6 +181,37 @@ int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, const uint8
                         const float* rotation, const float* centers, const float* qjl,
                         int merge, uint16_t* out, void* stream);
 
+/*
+ * Fused decode attention over a layer quantized in channel groups (the outlier split).
+ * The reference's fused kernel refuses such layers (runtime/triton_kernels.py:252-253) and
+ * its chunked path (runtime/attention.py:215-304) decodes K and V to bf16 for every step;
+ * this entry point replaces that path for them.
+ *
+ * n_groups (1 or 2) groups partition the dim channels; group g has sub_dims[g] channels,
+ * key_bits[g] / value_bits[g] (1..8) and the packed arrays k_codes[g] ... v_norms[g] in the
+ * channel-group layout above ([G][cap] rows of ceil(sub_dims[g]*bits/8) bytes; signs and
+ * rnorms only when has_qjl).  These six are HOST arrays of n_groups device pointers;
+ * sub_dims, key_bits and value_bits are host arrays too.  key_centers[g] /
+ * value_centers[g] are the groups' codebooks.
+ *
+ * key_matrix, qjl_matrix, value_matrix: [dim][dim] device matrices stacking the groups'
+ * channel-space matrices (tq_group_matrix), group 0's sub_dims[0] rows first.  The
+ * logits are scale * sum_g (|k_g| <q M_k rows of g, C_k,g[codes]> + sqrt(pi/2)/d_g |r_g|
+ * <q M_s rows of g, s_g>), the output (sum_t softmax_t |v_g,t| C_v,g[codes]) @ value_matrix.
+ * q, seq_starts, seq_lens, n_tokens, cap, scale, the outputs and the workspace (sized by
+ * tq_decode_attention_workspace_bytes) are as for tq_decode_attention.
+ */
+int tq_decode_attention_groups(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
+                               const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
+                               int n_groups, const int* sub_dims, const int* key_bits, const int* value_bits,
+                               int has_qjl, const uint8_t* const* k_codes, const uint16_t* const* k_norms,
+                               const uint8_t* const* k_signs, const uint16_t* const* k_rnorms,
+                               const uint8_t* const* v_codes, const uint16_t* const* v_norms,
+                               const float* key_matrix, const float* const* key_centers, const float* qjl_matrix,
+                               const float* value_matrix, const float* const* value_centers, float scale,
+                               float* out_f32, uint16_t* out_bf16, float* lse_out,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

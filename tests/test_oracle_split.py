@@ -85,6 +85,27 @@ def test_group_kernels_reject_bad_arguments_on_host():
     assert dq(out=ctypes.c_void_p((1 << 20) + 2)) == 2  # misaligned output rows
 
 
+def test_group_attention_rejects_bad_arguments_on_host():
+    lib = _lib.load()
+    P2 = ctypes.c_void_p * 2
+    I2 = ctypes.c_int * 2
+    ptrs = P2(FAKE, FAKE)
+
+    def call(n_groups=2, dims=(124, 4), kb=(3, 4), vb=(4, 5), qjl=1, q_heads=8, ws=FAKE, cap=16):
+        return lib.tq_decode_attention_groups(FAKE, 1, q_heads, 2, 128, None, None, 16, cap, n_groups, I2(*dims),
+                                              I2(*kb), I2(*vb), qjl, ptrs, ptrs, ptrs, ptrs, ptrs, ptrs, FAKE, ptrs,
+                                              FAKE, FAKE, ptrs, ctypes.c_float(0.0), FAKE, None, None, ws, 1 << 30,
+                                              None)
+
+    assert call(n_groups=3) == 1 and call(n_groups=0) == 1
+    assert call(dims=(120, 4)) == 1     # the groups must cover all 128 channels
+    assert call(kb=(3, 9)) == 1 and call(vb=(0, 5)) == 1
+    assert call(q_heads=9) == 1          # Hq not a multiple of Hkv
+    assert call(q_heads=18) == 2         # GQA group 9 > 8
+    assert call(ws=None) == 3
+    assert call(cap=8) == 1              # n_tokens > cap
+
+
 def test_group_wrappers_refuse_cpu_tensors():
     sc = split_codecs(np.arange(4, D), np.arange(4), 4, 1, 0, False, "cpu")
     x = torch.zeros(1, 1, 4, D, dtype=torch.bfloat16)

@@ -1025,6 +1025,297 @@ int dispatch(int value_bits, int has_qjl, int G, const SplitArgs& a, int groups,
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ------------------------------------------------------------------ channel-group layers
+// Decode attention over a layer whose channels are quantized in groups (the outlier split:
+// reference runtime/packed_qmse_cache.py:437-515; its fused kernel refuses such layers,
+// runtime/triton_kernels.py:252-253).  Group g has d_g channels, its own codebooks, bit
+// widths (1..8), norms and QJL sketch, in rows of ceil(d_g b / 8) bytes.  Stacking the
+// groups' channel-space matrices gives one D x D matrix per role whose row J < d_0 belongs to
+// group 0 and row J >= d_0 to group 1, so q R^T, q S^T and the final un-rotation are single
+// mat-vecs over one D-dimensional rotated space, and the partials (o[D], m, s) have the
+// split kernel's format: merge_kernel finishes the call with the stacked value matrix.
+//
+// group_attn_kernel: grid (n_split, batch * kv_heads), GT threads; per tile of GT tokens
+//   stage     the tile's key code and sign rows (then its value rows) into LDS with dword
+//             buffer loads: rows are not dword aligned, so codes are read from LDS at any
+//             bit offset (two dwords and an alignbit);
+//   scores    thread = token: sum over the group's codes of q_rot[J] C_g[code] times the
+//             token's group norm, plus the QJL term rho_g (2 sum_{s=1} q_proj - sum q_proj),
+//             for all heads of the GQA group at once (q_rot / q_proj broadcast from LDS);
+//   softmax   base 2, running maximum per head over the tiles;
+//   values    thread = (rotated dim J, token parity): o[J] += p |v_g| Cv_g[code_J].
+// Everything is fp32 VALU.
+
+constexpr int GT = 256;  // tokens per tile = threads per workgroup
+constexpr int NGRP = 2;  // channel groups per layer (at most)
+constexpr int GMAXC = 256;
+
+struct GroupAttnArgs {
+    const uint16_t* q;
+    int q_heads, kv_heads, G, n_groups;
+    const int32_t *seq_starts, *seq_lens;
+    int64_t n_tokens, cap;
+    const uint8_t* kc[NGRP];
+    const uint16_t* kn[NGRP];
+    const uint8_t* ks[NGRP];
+    const uint16_t* kr[NGRP];
+    const uint8_t* vc[NGRP];
+    const uint16_t* vn[NGRP];
+    int d[NGRP], j0[NGRP], kb[NGRP], vb[NGRP];
+    int rk[NGRP], rs[NGRP], rv[NGRP];  // row bytes: key codes, signs, value codes
+    const float* Ck[NGRP];
+    const float* Cv[NGRP];
+    float cq[NGRP];  // sqrt(pi/2)/d_g * scale * log2 e
+    float cs;        // scale * log2 e
+    const float *Mk, *Ms;  // stacked channel-space key / QJL matrices [D][D]
+    int kst[NGRP], sst[NGRP], vst[NGRP];  // LDS dword offsets of each staged row array
+    int64_t tps;
+    int n_split;
+    float *po, *pml;
+};
+
+// Staged dwords for one tile of rows of r bytes (the tile's first row may start mid-dword).
+__host__ __device__ inline int stage_dwords(int r) { return (GT * r + 3) / 4 + 2; }
+
+// Bits [bit, bit + n) (n <= 8) of the LDS dword array w.
+__device__ __forceinline__ uint32_t lds_bits(const uint32_t* w, uint32_t bit, uint32_t n) {
+    const uint32_t i = bit >> 5;
+    return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[i + 1], w[i], bit & 31), 0, n);
+}
+
+// Copies bytes [t0 r, (t0 + GT) r) of one (batch row, KV head)'s row array into LDS dwords
+// dst[0..], starting with the dword that holds byte t0 r; returns that byte's offset in dst.
+// `limit` = the array's bytes (cap r): dwords inside it are single loads, the last partial
+// dword is assembled from byte loads and nothing past it is read.
+__device__ __forceinline__ uint32_t stage_rows(uint32_t* dst, const uint8_t* base, uint32_t limit, uint32_t t0, int r,
+                                               int tid) {
+    const __amdgpu_buffer_rsrc_t rs = rsrc(base, limit);
+    const uint32_t b0 = t0 * (uint32_t)r;
+    const uint32_t a0 = b0 & ~3u;
+    const uint32_t n = (b0 + GT * (uint32_t)r - a0 + 3) >> 2;
+    for (uint32_t i = tid; i < n; i += GT) {
+        const uint32_t off = a0 + 4 * i;
+        uint32_t v = 0;
+        if (off + 4 <= limit) {
+            v = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        } else {
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k)
+                if (off + k < limit) v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, off + k, 0, 0) << (8 * k);
+        }
+        dst[i] = v;
+    }
+    return b0 - a0;
+}
+
+template <int GH, bool QJL>
+__global__ __launch_bounds__(GT) void group_attn_kernel(GroupAttnArgs a) {
+    extern __shared__ uint32_t stage[];
+    __shared__ float qr[D][GH];       // q R_k^T (stacked), times scale log2 e
+    __shared__ float qp[D][GH];       // q S^T (stacked), times the QJL scale of J's group
+    __shared__ float sqp[NGRP][GH];   // sum of qp over each group
+    __shared__ float ck[NGRP][GMAXC];
+    __shared__ float cv[NGRP][GMAXC];
+    __shared__ float wp[GH][GT];      // logits, then softmax weights, per (head, token)
+    __shared__ float vns[NGRP][GT];   // value norms of the tile's tokens (0 when invalid)
+    __shared__ float red[GT / 64][GH];
+    __shared__ float ored[GH][D];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x, grp = blockIdx.y;
+    const int b = grp / a.kv_heads, hk = grp % a.kv_heads;
+    const int G = a.G, ng = a.n_groups;
+
+    // ---- codebooks and the q-side mat-vecs
+    for (int g = 0; g < ng; ++g) {
+        for (int i = tid; i < (1 << a.kb[g]); i += GT) ck[g][i] = a.Ck[g][i];
+        for (int i = tid; i < (1 << a.vb[g]); i += GT) cv[g][i] = a.Cv[g][i];
+    }
+    const int nmv = (QJL ? 2 : 1) * GH * D;
+    for (int idx = tid; idx < nmv; idx += GT) {
+        const int which = idx / (GH * D), h = (idx / D) % GH, J = idx % D;
+        float acc = 0.0f;
+        if (h < G) {
+            const uint16_t* qh = a.q + ((size_t)b * a.q_heads + (size_t)hk * G + h) * D;
+            const float* m = (which ? a.Ms : a.Mk) + (size_t)J * D;
+            for (int c = 0; c < D; ++c) acc = __builtin_fmaf(tq::bf16_to_f32(qh[c]), m[c], acc);
+        }
+        const int g = (ng > 1 && J >= a.j0[1]) ? 1 : 0;
+        if (which) qp[J][h] = acc * a.cq[g];
+        else qr[J][h] = acc * a.cs;
+    }
+    __syncthreads();
+    if (QJL && tid < NGRP * GH) {
+        const int g = tid / GH, h = tid % GH;
+        float s = 0.0f;
+        if (g < ng)
+            for (int J = a.j0[g]; J < a.j0[g] + a.d[g]; ++J) s += qp[J][h];
+        sqp[g][h] = s;
+    }
+
+    // ---- this workgroup's valid token range
+    const int64_t t_begin = (int64_t)split * a.tps;
+    const int64_t t_end = t_begin + a.tps < a.n_tokens ? t_begin + a.tps : a.n_tokens;
+    const int64_t r_lo = a.seq_starts ? (int64_t)a.seq_starts[b] : 0;
+    const int64_t r_hi = a.seq_lens ? (int64_t)a.seq_lens[b] : a.n_tokens;
+    const int64_t lo = t_begin > r_lo ? t_begin : r_lo;
+    const int64_t hi = t_end < r_hi ? t_end : r_hi;
+
+    float M[GH], s_acc[GH], o_acc[GH];
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+        M[h] = NEG_INF;
+        s_acc[h] = 0.0f;
+        o_acc[h] = 0.0f;
+    }
+    const int vJ = tid & (D - 1), vpar = tid >> 7;
+    const int vg = (ng > 1 && vJ >= a.j0[1]) ? 1 : 0;
+    const int vj = vJ - a.j0[vg];
+    const int64_t gbase = (int64_t)grp * a.cap;
+
+    for (int64_t t0 = lo; t0 < hi; t0 += GT) {
+        const int nv = (int)(hi - t0 < GT ? hi - t0 : GT);
+        const bool valid = tid < nv;
+        const int64_t tok = t0 + tid;
+        // ---- stage key codes and signs
+        uint32_t koff[NGRP], soff[NGRP];
+        for (int g = 0; g < ng; ++g) {
+            koff[g] = stage_rows(stage + a.kst[g], a.kc[g] + gbase * a.rk[g], (uint32_t)(a.cap * a.rk[g]), (uint32_t)t0,
+                                 a.rk[g], tid);
+            if (QJL)
+                soff[g] = stage_rows(stage + a.sst[g], a.ks[g] + gbase * a.rs[g], (uint32_t)(a.cap * a.rs[g]),
+                                     (uint32_t)t0, a.rs[g], tid);
+        }
+        __syncthreads();
+        // ---- scores, thread = token
+        float l[GH];
+#pragma unroll
+        for (int h = 0; h < GH; ++h) l[h] = valid ? 0.0f : NEG_INF;
+        if (valid) {
+            for (int g = 0; g < ng; ++g) {
+                const uint32_t* ks = stage + a.kst[g];
+                const uint32_t bit0 = (koff[g] + (uint32_t)tid * a.rk[g]) * 8;
+                const uint32_t kb = a.kb[g];
+                float acc[GH];
+#pragma unroll
+                for (int h = 0; h < GH; ++h) acc[h] = 0.0f;
+                for (int j = 0; j < a.d[g]; ++j) {
+                    const float c = ck[g][lds_bits(ks, bit0 + j * kb, kb)];
+                    const int J = a.j0[g] + j;
+#pragma unroll
+                    for (int h = 0; h < GH; ++h) acc[h] = __builtin_fmaf(qr[J][h], c, acc[h]);
+                }
+                const float nk = tq::f16_to_f32(a.kn[g][gbase + tok]);
+#pragma unroll
+                for (int h = 0; h < GH; ++h) l[h] = __builtin_fmaf(nk, acc[h], l[h]);
+                if (QJL) {
+                    const uint32_t* ss = stage + a.sst[g];
+                    const uint32_t sb0 = (soff[g] + (uint32_t)tid * a.rs[g]) * 8;
+#pragma unroll
+                    for (int h = 0; h < GH; ++h) acc[h] = 0.0f;
+                    for (int j0 = 0; j0 < a.d[g]; j0 += 32) {
+                        const uint32_t i = (sb0 + j0) >> 5;
+                        uint32_t w = __builtin_amdgcn_alignbit(ss[i + 1], ss[i], (sb0 + j0) & 31);
+                        const int n = a.d[g] - j0 < 32 ? a.d[g] - j0 : 32;
+                        for (int jj = 0; jj < n; ++jj, w >>= 1) {
+                            const float f = (float)(w & 1u);
+                            const int J = a.j0[g] + j0 + jj;
+#pragma unroll
+                            for (int h = 0; h < GH; ++h) acc[h] = __builtin_fmaf(f, qp[J][h], acc[h]);
+                        }
+                    }
+                    const float rn = tq::f16_to_f32(a.kr[g][gbase + tok]);
+#pragma unroll
+                    for (int h = 0; h < GH; ++h) l[h] = __builtin_fmaf(rn, 2.0f * acc[h] - sqp[g][h], l[h]);
+                }
+            }
+        }
+        // ---- tile maximum per head
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            float m = l[h];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            if (lane == 0) red[wave][h] = m;
+        }
+        __syncthreads();  // key stage consumed, tile maxima visible
+        // ---- stage value codes; weights and value norms of the thread's token
+        uint32_t voff[NGRP];
+        for (int g = 0; g < ng; ++g)
+            voff[g] = stage_rows(stage + a.vst[g], a.vc[g] + gbase * a.rv[g], (uint32_t)(a.cap * a.rv[g]),
+                                 (uint32_t)t0, a.rv[g], tid);
+        float alpha[GH];
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            float m = red[0][h];
+#pragma unroll
+            for (int w = 1; w < GT / 64; ++w) m = fmaxf(m, red[w][h]);
+            const float nm = fmaxf(M[h], m);
+            alpha[h] = nm == NEG_INF ? 1.0f : __builtin_amdgcn_exp2f(M[h] - nm);
+            M[h] = nm;
+            const float p = valid ? __builtin_amdgcn_exp2f(l[h] - nm) : 0.0f;
+            s_acc[h] = __builtin_fmaf(s_acc[h], alpha[h], p);
+            wp[h][tid] = p;
+        }
+        for (int g = 0; g < ng; ++g) vns[g][tid] = valid ? tq::f16_to_f32(a.vn[g][gbase + tok]) : 0.0f;
+        __syncthreads();
+        // ---- values, thread = (rotated dim, token parity)
+        {
+            const uint32_t* vs = stage + a.vst[vg];
+            const uint32_t vb = a.vb[vg], rv = a.rv[vg];
+            const uint32_t bitj = voff[vg] * 8 + (uint32_t)vj * vb;
+#pragma unroll
+            for (int h = 0; h < GH; ++h) o_acc[h] *= alpha[h];
+            for (int tt = vpar; tt < nv; tt += 2) {
+                const float v = vns[vg][tt] * cv[vg][lds_bits(vs, bitj + (uint32_t)tt * rv * 8, vb)];
+#pragma unroll
+                for (int h = 0; h < GH; ++h) o_acc[h] = __builtin_fmaf(wp[h][tt], v, o_acc[h]);
+            }
+        }
+        __syncthreads();  // stage, wp and vns are rewritten by the next tile
+    }
+
+    // ---- partials (o[D], m, s) per query head
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+        float s = s_acc[h];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        if (lane == 0) red[wave][h] = s;
+    }
+    if (vpar) {
+#pragma unroll
+        for (int h = 0; h < GH; ++h) ored[h][vJ] = o_acc[h];
+    }
+    __syncthreads();
+    if (!vpar) {
+        for (int h = 0; h < G; ++h) {
+            const size_t pidx = ((size_t)b * a.q_heads + (size_t)hk * G + h) * a.n_split + split;
+            a.po[pidx * D + vJ] = o_acc[h] + ored[h][vJ];
+            if (vJ == 0) {
+                float s = 0.0f;
+#pragma unroll
+                for (int w = 0; w < GT / 64; ++w) s += red[w][h];
+                a.pml[pidx * 2 + 0] = M[h];
+                a.pml[pidx * 2 + 1] = s;
+            }
+        }
+    }
+}
+
+int group_split(int groups, int64_t n_tokens, int64_t* tps) {
+    const int64_t max_split = (n_tokens + GT - 1) / GT;
+    int64_t ns = (MAX_WGS + groups - 1) / groups;
+    if (ns > max_split) ns = max_split;
+    if (ns < 1) ns = 1;
+    int64_t per = (n_tokens + ns - 1) / ns;
+    per = (per + GT - 1) / GT * GT;
+    if (per < GT) per = GT;
+    *tps = per;
+    const int64_t got = (n_tokens + per - 1) / per;
+    return (int)(got > 0 ? got : 1);
+}
+
 }  // namespace
 
 extern "C" size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, int kv_heads, int dim,
@@ -1084,6 +1375,107 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
     if (st != TQ_OK) return st;
     TQ_CHECK_LAUNCH();
     hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(MT), 0, s, a.po, a.pml, n_split, value_rotation,
+                       out_f32, out_bf16, lse_out);
+    TQ_CHECK_LAUNCH();
+    return TQ_OK;
+}
+
+extern "C" int tq_decode_attention_groups(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
+                                          const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens,
+                                          int64_t cap, int n_groups, const int* sub_dims, const int* key_bits,
+                                          const int* value_bits, int has_qjl, const uint8_t* const* k_codes,
+                                          const uint16_t* const* k_norms, const uint8_t* const* k_signs,
+                                          const uint16_t* const* k_rnorms, const uint8_t* const* v_codes,
+                                          const uint16_t* const* v_norms, const float* key_matrix,
+                                          const float* const* key_centers, const float* qjl_matrix,
+                                          const float* value_matrix, const float* const* value_centers, float scale,
+                                          float* out_f32, uint16_t* out_bf16, float* lse_out, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+    if (!q || batch <= 0 || q_heads <= 0 || kv_heads <= 0 || n_tokens < 0 || cap < n_tokens)
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (dim != D) return TQ_ERR_UNSUPPORTED;
+    if (q_heads % kv_heads) return TQ_ERR_INVALID_ARGUMENT;
+    const int G = q_heads / kv_heads;
+    if (G > TQ_MAX_GROUP) return TQ_ERR_UNSUPPORTED;
+    if (n_groups < 1 || n_groups > NGRP || !sub_dims || !key_bits || !value_bits || !k_codes || !k_norms ||
+        !v_codes || !v_norms || !key_centers || !value_centers)
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (!key_matrix || !value_matrix || (has_qjl && (!qjl_matrix || !k_signs || !k_rnorms)))
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (!out_f32 && !out_bf16 && !lse_out) return TQ_ERR_INVALID_ARGUMENT;
+    if (!workspace) return TQ_ERR_WORKSPACE;
+    if (!(scale > 0.0f)) scale = 1.0f / sqrtf((float)D);
+    GroupAttnArgs a{};
+    a.q = q;
+    a.q_heads = q_heads;
+    a.kv_heads = kv_heads;
+    a.G = G;
+    a.n_groups = n_groups;
+    a.seq_starts = seq_starts;
+    a.seq_lens = seq_lens;
+    a.n_tokens = n_tokens;
+    a.cap = cap;
+    a.cs = scale * LOG2E;
+    a.Mk = key_matrix;
+    a.Ms = qjl_matrix;
+    int dsum = 0, kst = 0, vst = 0;
+    for (int g = 0; g < n_groups; ++g) {
+        const int d = sub_dims[g], kb = key_bits[g], vb = value_bits[g];
+        if (d < 1 || kb < 1 || kb > 8 || vb < 1 || vb > 8) return TQ_ERR_INVALID_ARGUMENT;
+        if (!k_codes[g] || !k_norms[g] || !v_codes[g] || !v_norms[g] || !key_centers[g] || !value_centers[g])
+            return TQ_ERR_INVALID_ARGUMENT;
+        if (has_qjl && (!k_signs[g] || !k_rnorms[g])) return TQ_ERR_INVALID_ARGUMENT;
+        a.kc[g] = k_codes[g];
+        a.kn[g] = k_norms[g];
+        a.ks[g] = has_qjl ? k_signs[g] : nullptr;
+        a.kr[g] = has_qjl ? k_rnorms[g] : nullptr;
+        a.vc[g] = v_codes[g];
+        a.vn[g] = v_norms[g];
+        a.d[g] = d;
+        a.j0[g] = dsum;
+        a.kb[g] = kb;
+        a.vb[g] = vb;
+        a.rk[g] = (d * kb + 7) / 8;
+        a.rs[g] = (d + 7) / 8;
+        a.rv[g] = (d * vb + 7) / 8;
+        a.Ck[g] = key_centers[g];
+        a.Cv[g] = value_centers[g];
+        a.cq[g] = scale * LOG2E * (float)(sqrt(M_PI / 2.0) / (double)d);
+        // every byte offset of the group's rows, including one tile past the capacity, fits
+        // the 31-bit buffer range and 32-bit offsets
+        const int64_t rmax = a.rk[g] > a.rv[g] ? a.rk[g] : a.rv[g];
+        if ((cap + GT) * rmax >= ((int64_t)1 << 31)) return TQ_ERR_UNSUPPORTED;
+        a.kst[g] = kst;
+        kst += stage_dwords(a.rk[g]);
+        a.sst[g] = kst;
+        if (has_qjl) kst += stage_dwords(a.rs[g]);
+        a.vst[g] = vst;
+        vst += stage_dwords(a.rv[g]);
+        dsum += d;
+    }
+    if (dsum != D) return TQ_ERR_INVALID_ARGUMENT;  // the groups partition the head's channels
+    const int groups = batch * kv_heads;
+    int64_t tps = 0;
+    const int n_split = group_split(groups, n_tokens > 0 ? n_tokens : 1, &tps);
+    const Ws w = ws_layout(batch, q_heads, n_split);
+    if (workspace_bytes < w.total) return TQ_ERR_WORKSPACE;
+    char* base = static_cast<char*>(workspace);
+    a.po = reinterpret_cast<float*>(base + w.po);
+    a.pml = reinterpret_cast<float*>(base + w.pml);
+    a.tps = tps;
+    a.n_split = n_split;
+    const size_t lds = (size_t)(kst > vst ? kst : vst) * sizeof(uint32_t);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(n_split, groups);
+    if (G <= 4) {
+        if (has_qjl) hipLaunchKernelGGL((group_attn_kernel<4, true>), grid, dim3(GT), lds, s, a);
+        else hipLaunchKernelGGL((group_attn_kernel<4, false>), grid, dim3(GT), lds, s, a);
+    } else {
+        if (has_qjl) hipLaunchKernelGGL((group_attn_kernel<8, true>), grid, dim3(GT), lds, s, a);
+        else hipLaunchKernelGGL((group_attn_kernel<8, false>), grid, dim3(GT), lds, s, a);
+    }
+    TQ_CHECK_LAUNCH();
+    hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(MT), 0, s, a.po, a.pml, n_split, value_matrix,
                        out_f32, out_bf16, lse_out);
     TQ_CHECK_LAUNCH();
     return TQ_OK;

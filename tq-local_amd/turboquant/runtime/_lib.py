@@ -35,6 +35,8 @@ SIGNATURES: dict[str, tuple] = {
     "tq_dequantize_mse": (_I, [_P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "tq_dequantize_prod": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P]),
     "tq_group_matrix": (_I, [_P, _I, _P, _I, _P]),
+    "tq_decode_attention_groups": (_I, [_P, _I, _I, _I, _I, _P, _P, _I64, _I64, _I, _P, _P, _P, _I, _P, _P, _P, _P,
+                                        _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _SZ, _P]),
     "tq_quantize_group": (_I, [_P, _I, _I, _I64, _I, _I64, _I64, _I64, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P,
                                _P, _I64, _I64, _P]),
     "tq_dequantize_group": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _I, _I, _P, _P, _P, _I, _P, _P]),

@@ -11,11 +11,11 @@ layers) it is plain SDPA, as in the reference.
 batch size (one query token per row) and honours left/right padding from the
 attention mask; it has no fallback path -- shapes it does not cover raise.
 
-Outlier-split layers take ``split_attention``: the reference's fused kernel
-refuses them (``triton_kernels.py:252-253``) and its chunked path
-(``runtime/attention.py:215-304``) decodes K and V to bf16 and runs exact
-softmax attention; here libtq's channel-group kernels do the decoding and the
-softmax runs in fp32 on the device.
+Outlier-split layers run libtq's channel-group attention kernel
+(``tq_decode_attention_groups``), which scores each channel group in its own
+rotated space; the reference's fused kernel refuses such layers
+(``triton_kernels.py:252-253``) and its chunked path
+(``runtime/attention.py:215-304``) dequantises K and V for every step instead.
 """
 
 from __future__ import annotations
@@ -58,32 +58,49 @@ def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device
     return starts.to(device=device, dtype=torch.int32), ends.to(device=device, dtype=torch.int32)
 
 
+def _group_buffers(layer: "PackedMSELayer") -> list[dict]:
+    """The store's capacity buffers of each channel group of a split layer."""
+    s, sc = layer._store, layer._split
+    qjl = sc.use_qjl_keys
+    out = []
+    for sfx, kg, vg in (("", sc.key_normal, sc.value_normal), ("o", sc.key_outlier, sc.value_outlier)):
+        out.append({"key": kg, "value": vg, "k_codes": getattr(s, "kc" + sfx), "k_norms": getattr(s, "kn" + sfx),
+                    "k_signs": getattr(s, "ks" + sfx) if qjl else None,
+                    "k_rnorms": getattr(s, "kr" + sfx) if qjl else None,
+                    "v_codes": getattr(s, "vc" + sfx), "v_norms": getattr(s, "vn" + sfx)})
+    return out
+
+
 def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", n_kv_groups: int,
                     attention_mask: torch.Tensor | None = None) -> torch.Tensor:
     """Decode attention of [B, Hq, 1, D] queries over a packed layer -> [B, Hq, 1, D].
 
     The logit scale is 1/sqrt(D) (reference ``triton_kernels.py:285``).  Tokens
-    kept dense (``quantize_decode=False``) are merged by log-sum-exp.  An
-    outlier-split layer is handed to ``split_attention`` (where the reference
-    returns None and its caller takes the chunked path).
+    kept dense (``quantize_decode=False``) are merged by log-sum-exp.  Outlier-split
+    layers go through the channel-group kernel (where the reference returns None and
+    its caller takes the chunked path).
     """
-    if packed_layer._outlier_enabled:
-        return split_attention(query_states, packed_layer, n_kv_groups, attention_mask)
     B, Hq, Sq, D = query_states.shape
     if Sq != 1:
         raise NotImplementedError("TurboQuant fused attention takes one decode token per sequence "
                                   f"(got {Sq}); prefill runs dense SDPA before the cache is packed")
     store = packed_layer._store
-    c = packed_layer.codecs
     n_packed = packed_layer.packed_seq_length()
     n_dense = 0 if packed_layer._dense_keys is None else int(packed_layer._dense_keys.shape[-2])
     scale = 1.0 / math.sqrt(D)
     starts, ends = _valid_range(attention_mask, B, n_packed + n_dense, query_states.device)
     p_ends = None if ends is None else torch.clamp(ends, max=n_packed)
-    outs = K.decode_attention(query_states, k_codes=store.kc, k_norms=store.kn, v_codes=store.vc, v_norms=store.vn,
-                              n_tokens=n_packed, key=c.key, value=c.value, k_signs=store.ks, k_rnorms=store.kr,
-                              qjl=c.qjl, seq_starts=starts, seq_lens=p_ends, scale=scale, want_f32=n_dense > 0,
-                              want_lse=n_dense > 0)
+    kw = dict(n_tokens=n_packed, seq_starts=starts, seq_lens=p_ends, scale=scale, want_f32=n_dense > 0,
+              want_lse=n_dense > 0)
+    if packed_layer._outlier_enabled:
+        sc = packed_layer._split
+        outs = K.decode_attention_groups(query_states, _group_buffers(packed_layer), key_stack=sc.key_stack,
+                                         value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, **kw)
+    else:
+        c = packed_layer.codecs
+        outs = K.decode_attention(query_states, k_codes=store.kc, k_norms=store.kn, v_codes=store.vc,
+                                  v_norms=store.vn, key=c.key, value=c.value, k_signs=store.ks, k_rnorms=store.kr,
+                                  qjl=c.qjl, **kw)
     if n_dense == 0:
         return outs.to(query_states.dtype).view(B, Hq, 1, D)
     _, o_packed, lse_packed = outs
@@ -103,37 +120,6 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
     num = o_packed * wp[..., None] + (wd[..., None] * dv).sum(dim=2)
     den = (wp + wd.sum(dim=-1)).clamp(min=1e-30)[..., None]
     return (num / den).to(query_states.dtype).view(B, Hq, 1, D)
-
-
-def split_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", n_kv_groups: int,
-                    attention_mask: torch.Tensor | None = None) -> torch.Tensor:
-    """Decode attention of [B, Hq, 1, D] queries over an outlier-split layer -> [B, Hq, 1, D].
-
-    K^ and V^ are the bf16 rows of both channel groups decoded by libtq (reference
-    ``_decode_keys_range`` / ``_decode_values_range``, runtime/packed_qmse_cache.py:564-592),
-    followed by the dense decode buffer; logits are fp32 ``q . K^ / sqrt(D)``, the
-    softmax is exact and the normaliser is clamped at 1e-8 (runtime/attention.py:189-304).
-    """
-    B, Hq, Sq, D = query_states.shape
-    if Sq != 1:
-        raise NotImplementedError(f"TurboQuant decode attention takes one token per sequence (got {Sq})")
-    keys, values = packed_layer._decode_keys_full(), packed_layer._decode_values_full()
-    if packed_layer._dense_keys is not None:
-        keys = torch.cat((keys, packed_layer._dense_keys.to(keys.dtype)), dim=-2)
-        values = torch.cat((values, packed_layer._dense_values.to(values.dtype)), dim=-2)
-    Hkv, N = keys.shape[1], keys.shape[2]
-    q = query_states.float().reshape(B, Hkv, n_kv_groups, D)  # query head h reads KV head h // groups
-    logits = torch.matmul(q, keys.float().transpose(-2, -1)) * (1.0 / math.sqrt(D))  # [B, Hkv, G, N]
-    starts, ends = _valid_range(attention_mask, B, N, query_states.device)
-    if starts is not None:
-        pos = torch.arange(N, device=logits.device)
-        ok = (pos[None, :] >= starts[:, None]) & (pos[None, :] < ends[:, None])
-        logits = logits.masked_fill(~ok[:, None, None, :], float("-inf"))
-    m = logits.amax(dim=-1, keepdim=True)
-    m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
-    p = torch.exp(logits - m)
-    out = torch.matmul(p, values.float()) / p.sum(dim=-1, keepdim=True).clamp(min=1e-8)
-    return out.reshape(B, Hq, 1, D).to(query_states.dtype)
 
 
 def _sdpa_fallback(module, query, key, value, attention_mask, scaling):

@@ -13,6 +13,9 @@ Reference interfaces replaced:
                                                            runtime/packed_qmse_cache.py:481-496, 437-454
   dequantize_group -> PackedMSELayer._decode_merge / _decode_keys_merge_qjl (one channel group)
                                                            runtime/packed_qmse_cache.py:498-515, 456-479
+  decode_attention_groups -> the reference's attention over outlier-split layers, which its
+                    fused kernel refuses (runtime/triton_kernels.py:252-253) and its chunked
+                    path dequantises (runtime/attention.py:215-304)
 """
 
 from __future__ import annotations
@@ -256,5 +259,65 @@ def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.T
               key.bits, value.bits, int(has_qjl), _vp(key.rotation), _vp(key.centers), _vp(qjl),
               _vp(value.rotation), _vp(value.centers), ctypes.c_float(s), _vp(out_f32), _vp(out_bf16),
               _vp(lse), _vp(ws), ws.numel(), _stream(q.device))
+    outs = (out_bf16,) + ((out_f32,) if want_f32 else ()) + ((lse,) if want_lse else ())
+    return outs if len(outs) > 1 else out_bf16
+
+
+def decode_attention_groups(q: torch.Tensor, groups: list[dict], *, n_tokens: int, key_stack: torch.Tensor,
+                            value_stack: torch.Tensor, qjl_stack: torch.Tensor | None = None,
+                            seq_lens: torch.Tensor | None = None, seq_starts: torch.Tensor | None = None,
+                            scale: float | None = None, want_f32: bool = False, want_lse: bool = False):
+    """Fused decode attention over a layer quantized in channel groups (the outlier split).
+
+    ``groups``: per group a dict with ``key`` / ``value`` (GroupCodec), ``k_codes``,
+    ``k_norms``, ``v_codes``, ``v_norms`` and, with QJL, ``k_signs`` / ``k_rnorms``, each
+    [B, Hkv, cap, ...].  ``key_stack`` / ``value_stack`` / ``qjl_stack`` are the groups'
+    channel-space matrices stacked into D x D.  Returns as ``decode_attention``.
+    """
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise ValueError("decode_attention_groups takes exactly one query token per sequence")
+        q = q[:, :, 0, :]
+    q = q.to(torch.bfloat16).contiguous()
+    first = groups[0]
+    _require_gpu(q, first["k_codes"], first["v_codes"], key_stack, value_stack)
+    B, Hq, D = q.shape
+    Hkv, cap = first["k_codes"].shape[1], first["k_codes"].shape[2]
+    has_qjl = qjl_stack is not None
+    n = len(groups)
+
+    def arr(ctype, values):
+        return (ctype * n)(*values)
+
+    P = ctypes.c_void_p
+    keep = []  # ctypes arrays must outlive the call
+    for g in groups:
+        for name in ("k_codes", "k_norms", "v_codes", "v_norms") + (("k_signs", "k_rnorms") if has_qjl else ()):
+            t = g[name]
+            if t.shape[:3] != (B, Hkv, cap) or not t.is_contiguous():
+                raise ValueError(f"{name}: expected a contiguous [B, Hkv, cap, ...] buffer, got {tuple(t.shape)}")
+    dims = arr(ctypes.c_int, [g["key"].dim for g in groups])
+    kbits = arr(ctypes.c_int, [g["key"].bits for g in groups])
+    vbits = arr(ctypes.c_int, [g["value"].bits for g in groups])
+    ptr = lambda name: arr(P, [g[name].data_ptr() if g.get(name) is not None else None for g in groups])  # noqa: E731
+    kc, kn, vc, vn = ptr("k_codes"), ptr("k_norms"), ptr("v_codes"), ptr("v_norms")
+    ks = ptr("k_signs") if has_qjl else None
+    kr = ptr("k_rnorms") if has_qjl else None
+    ck = arr(P, [g["key"].centers.data_ptr() for g in groups])
+    cv = arr(P, [g["value"].centers.data_ptr() for g in groups])
+    keep += [dims, kbits, vbits, kc, kn, vc, vn, ks, kr, ck, cv]
+    out_bf16 = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=q.device)
+    out_f32 = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device) if want_f32 else None
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=q.device) if want_lse else None
+    ws = attention_workspace(q.device, B, Hq, Hkv, max(int(n_tokens), 1))
+    if seq_lens is not None:
+        seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
+    if seq_starts is not None:
+        seq_starts = seq_starts.to(device=q.device, dtype=torch.int32).contiguous()
+    s = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    _lib.call("tq_decode_attention_groups", _vp(q), B, Hq, Hkv, D, _vp(seq_starts), _vp(seq_lens), int(n_tokens), cap,
+              n, dims, kbits, vbits, int(has_qjl), kc, kn, ks, kr, vc, vn, _vp(key_stack), ck, _vp(qjl_stack),
+              _vp(value_stack), cv, ctypes.c_float(s), _vp(out_f32), _vp(out_bf16), _vp(lse), _vp(ws), ws.numel(),
+              _stream(q.device))
     outs = (out_bf16,) + ((out_f32,) if want_f32 else ()) + ((lse,) if want_lse else ())
     return outs if len(outs) > 1 else out_bf16

@@ -110,6 +110,11 @@ class SplitCodecs:
     value_outlier: GroupCodec
     key_normal: GroupCodec  # the value groups themselves for Q_mse keys
     key_outlier: GroupCodec
+    # the groups' channel-space matrices stacked into one D x D matrix per role (rows of the
+    # normal group first): the rotated space of tq_decode_attention_groups
+    key_stack: torch.Tensor
+    value_stack: torch.Tensor
+    qjl_stack: torch.Tensor | None
 
 
 def _group(channels: np.ndarray, bits: int, seed: int, device: torch.device, grid_size: int,
@@ -158,9 +163,12 @@ def split_codecs(normal_channels, outlier_channels, bits: int, outlier_extra_bit
                     qjl_seed=seed + QJL_SEED_OFFSET + 1)
     else:
         kn, ko = vn, vo
+    stack = lambda a, b: torch.cat((a[:len(normal)], b[:len(outlier)])).contiguous()  # noqa: E731
     out = SplitCodecs(bits=bits, outlier_bits=outlier_bits, use_qjl_keys=use_qjl_keys,
                       normal_indices=torch.from_numpy(normal.astype(np.int64)).to(device),
                       outlier_indices=torch.from_numpy(outlier.astype(np.int64)).to(device),
-                      value_normal=vn, value_outlier=vo, key_normal=kn, key_outlier=ko)
+                      value_normal=vn, value_outlier=vo, key_normal=kn, key_outlier=ko,
+                      key_stack=stack(kn.rotation_ch, ko.rotation_ch), value_stack=stack(vn.rotation_ch, vo.rotation_ch),
+                      qjl_stack=stack(kn.qjl_ch, ko.qjl_ch) if use_qjl_keys else None)
     _split_cache[key] = out
     return out
