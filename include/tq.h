@@ -194,8 +194,9 @@ int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, const uint8
  * sub_dims, key_bits and value_bits are host arrays too.  key_centers[g] /
  * value_centers[g] are the groups' codebooks.
  *
- * key_matrix, qjl_matrix, value_matrix: [dim][dim] device matrices stacking the groups'
- * channel-space matrices (tq_group_matrix), group 0's sub_dims[0] rows first.  The
+ * key_matrix, qjl_matrix, value_matrix: [dim][dim] device matrices (16-byte aligned)
+ * stacking the groups' channel-space matrices (tq_group_matrix), group 0's sub_dims[0]
+ * rows first.  The
  * logits are scale * sum_g (|k_g| <q M_k rows of g, C_k,g[codes]> + sqrt(pi/2)/d_g |r_g|
  * <q M_s rows of g, s_g>), the output (sum_t softmax_t |v_g,t| C_v,g[codes]) @ value_matrix.
  * q, seq_starts, seq_lens, n_tokens, cap, scale, the outputs and the workspace (sized by

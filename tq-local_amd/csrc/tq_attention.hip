@@ -1093,16 +1093,17 @@ __device__ __forceinline__ uint32_t stage_rows(uint32_t* dst, const uint8_t* bas
     const uint32_t b0 = t0 * (uint32_t)r;
     const uint32_t a0 = b0 & ~3u;
     const uint32_t n = (b0 + GT * (uint32_t)r - a0 + 3) >> 2;
-    for (uint32_t i = tid; i < n; i += GT) {
+    const uint32_t whole = (limit - a0) >> 2;  // dwords wholly inside the array (a0 <= b0 < limit)
+    const uint32_t nf = n < whole ? n : whole;
+    // independent loads, several in flight per thread
+#pragma unroll 8
+    for (uint32_t i = tid; i < nf; i += GT) dst[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, a0 + 4 * i, 0, 0);
+    for (uint32_t i = nf + tid; i < n; i += GT) {  // the array's last partial dword, then zeros
         const uint32_t off = a0 + 4 * i;
         uint32_t v = 0;
-        if (off + 4 <= limit) {
-            v = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
-        } else {
 #pragma unroll
-            for (uint32_t k = 0; k < 4; ++k)
-                if (off + k < limit) v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, off + k, 0, 0) << (8 * k);
-        }
+        for (uint32_t k = 0; k < 4; ++k)
+            if (off + k < limit) v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, off + k, 0, 0) << (8 * k);
         dst[i] = v;
     }
     return b0 - a0;
@@ -1116,7 +1117,7 @@ __global__ __launch_bounds__(GT) void group_attn_kernel(GroupAttnArgs a) {
     __shared__ float sqp[NGRP][GH];   // sum of qp over each group
     __shared__ float ck[NGRP][GMAXC];
     __shared__ float cv[NGRP][GMAXC];
-    __shared__ float wp[GH][GT];      // logits, then softmax weights, per (head, token)
+    __shared__ float wp[GT][GH];      // softmax weights per (token, head): one broadcast read per token
     __shared__ float vns[NGRP][GT];   // value norms of the tile's tokens (0 when invalid)
     __shared__ float red[GT / 64][GH];
     __shared__ float ored[GH][D];
@@ -1131,18 +1132,35 @@ __global__ __launch_bounds__(GT) void group_attn_kernel(GroupAttnArgs a) {
         for (int i = tid; i < (1 << a.kb[g]); i += GT) ck[g][i] = a.Ck[g][i];
         for (int i = tid; i < (1 << a.vb[g]); i += GT) cv[g][i] = a.Cv[g][i];
     }
-    const int nmv = (QJL ? 2 : 1) * GH * D;
-    for (int idx = tid; idx < nmv; idx += GT) {
-        const int which = idx / (GH * D), h = (idx / D) % GH, J = idx % D;
-        float acc = 0.0f;
-        if (h < G) {
-            const uint16_t* qh = a.q + ((size_t)b * a.q_heads + (size_t)hk * G + h) * D;
-            const float* m = (which ? a.Ms : a.Mk) + (size_t)J * D;
-            for (int c = 0; c < D; ++c) acc = __builtin_fmaf(tq::bf16_to_f32(qh[c]), m[c], acc);
+    // the group's queries in fp32, channel-major (in wp, which the tiles overwrite later)
+    float(*qsh)[GH] = reinterpret_cast<float(*)[GH]>(&wp[0][0]);
+    for (int i = tid; i < GH * D; i += GT) {
+        const int h = i / D, c = i % D;
+        qsh[c][h] = h < G ? tq::bf16_to_f32(a.q[((size_t)b * a.q_heads + (size_t)hk * G + h) * D + c]) : 0.0f;
+    }
+    __syncthreads();
+    // thread (matrix, rotated dim J): row J of M_k (or M_s) against every head, 16-byte row reads
+    if (tid < (QJL ? 2 : 1) * D) {
+        const int which = tid / D, J = tid % D;
+        const float4* m4 = reinterpret_cast<const float4*>((which ? a.Ms : a.Mk) + (size_t)J * D);
+        float acc[GH];
+#pragma unroll
+        for (int h = 0; h < GH; ++h) acc[h] = 0.0f;
+#pragma unroll 2
+        for (int c4 = 0; c4 < D / 4; ++c4) {
+            const float4 m = m4[c4];
+            const float mv[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int h = 0; h < GH; ++h) acc[h] = __builtin_fmaf(qsh[4 * c4 + k][h], mv[k], acc[h]);
         }
         const int g = (ng > 1 && J >= a.j0[1]) ? 1 : 0;
-        if (which) qp[J][h] = acc * a.cq[g];
-        else qr[J][h] = acc * a.cs;
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            if (which) qp[J][h] = acc[h] * a.cq[g];
+            else qr[J][h] = acc[h] * a.cs;
+        }
     }
     __syncthreads();
     if (QJL && tid < NGRP * GH) {
@@ -1199,6 +1217,7 @@ __global__ __launch_bounds__(GT) void group_attn_kernel(GroupAttnArgs a) {
                 float acc[GH];
 #pragma unroll
                 for (int h = 0; h < GH; ++h) acc[h] = 0.0f;
+#pragma unroll 4
                 for (int j = 0; j < a.d[g]; ++j) {
                     const float c = ck[g][lds_bits(ks, bit0 + j * kb, kb)];
                     const int J = a.j0[g] + j;
@@ -1217,6 +1236,7 @@ __global__ __launch_bounds__(GT) void group_attn_kernel(GroupAttnArgs a) {
                         const uint32_t i = (sb0 + j0) >> 5;
                         uint32_t w = __builtin_amdgcn_alignbit(ss[i + 1], ss[i], (sb0 + j0) & 31);
                         const int n = a.d[g] - j0 < 32 ? a.d[g] - j0 : 32;
+#pragma unroll 4
                         for (int jj = 0; jj < n; ++jj, w >>= 1) {
                             const float f = (float)(w & 1u);
                             const int J = a.j0[g] + j0 + jj;
@@ -1255,7 +1275,7 @@ __global__ __launch_bounds__(GT) void group_attn_kernel(GroupAttnArgs a) {
             M[h] = nm;
             const float p = valid ? __builtin_amdgcn_exp2f(l[h] - nm) : 0.0f;
             s_acc[h] = __builtin_fmaf(s_acc[h], alpha[h], p);
-            wp[h][tid] = p;
+            wp[tid][h] = p;
         }
         for (int g = 0; g < ng; ++g) vns[g][tid] = valid ? tq::f16_to_f32(a.vn[g][gbase + tok]) : 0.0f;
         __syncthreads();
@@ -1266,10 +1286,11 @@ __global__ __launch_bounds__(GT) void group_attn_kernel(GroupAttnArgs a) {
             const uint32_t bitj = voff[vg] * 8 + (uint32_t)vj * vb;
 #pragma unroll
             for (int h = 0; h < GH; ++h) o_acc[h] *= alpha[h];
+#pragma unroll 4
             for (int tt = vpar; tt < nv; tt += 2) {
                 const float v = vns[vg][tt] * cv[vg][lds_bits(vs, bitj + (uint32_t)tt * rv * 8, vb)];
 #pragma unroll
-                for (int h = 0; h < GH; ++h) o_acc[h] = __builtin_fmaf(wp[h][tt], v, o_acc[h]);
+                for (int h = 0; h < GH; ++h) o_acc[h] = __builtin_fmaf(wp[tt][h], v, o_acc[h]);
             }
         }
         __syncthreads();  // stage, wp and vns are rewritten by the next tile
@@ -1402,6 +1423,8 @@ extern "C" int tq_decode_attention_groups(const uint16_t* q, int batch, int q_he
         return TQ_ERR_INVALID_ARGUMENT;
     if (!key_matrix || !value_matrix || (has_qjl && (!qjl_matrix || !k_signs || !k_rnorms)))
         return TQ_ERR_INVALID_ARGUMENT;
+    if (!aligned16(key_matrix) || !aligned16(value_matrix) || (has_qjl && !aligned16(qjl_matrix)))
+        return TQ_ERR_UNSUPPORTED;  // rows are read as float4
     if (!out_f32 && !out_bf16 && !lse_out) return TQ_ERR_INVALID_ARGUMENT;
     if (!workspace) return TQ_ERR_WORKSPACE;
     if (!(scale > 0.0f)) scale = 1.0f / sqrtf((float)D);
