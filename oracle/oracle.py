@@ -70,10 +70,11 @@ def lib() -> ctypes.CDLL:
         L.tq_oracle_decode_mse.argtypes = [P, P, I64, I, I, P, P, P]
         L.tq_oracle_rotated.argtypes = [P, I64, I, P, P]
         L.tq_oracle_decode_prod.argtypes = [P, P, P, P, I64, I, I, P, P, P, P]
+        L.tq_oracle_norms.argtypes = [P, I64, I, P]
         L.tq_oracle_f32_to_f16_array.argtypes = [P, I64, P]
         L.tq_oracle_f32_to_bf16_array.argtypes = [P, I64, P]
         for fn in ("tq_oracle_encode_mse", "tq_oracle_encode_prod", "tq_oracle_decode_mse", "tq_oracle_decode_prod",
-                   "tq_oracle_rotated", "tq_oracle_f32_to_f16_array", "tq_oracle_f32_to_bf16_array"):
+                   "tq_oracle_rotated", "tq_oracle_norms", "tq_oracle_f32_to_f16_array", "tq_oracle_f32_to_bf16_array"):
             getattr(L, fn).restype = None
         _lib = L
     return _lib
@@ -183,6 +184,15 @@ def decode_prod(codes, norms, signs, rnorms, mse_bits: int, dim: int, R, centers
                                 m, dim, mse_bits, _p(np.ascontiguousarray(R, np.float32)),
                                 _p(np.ascontiguousarray(centers, np.float32)), _p(np.ascontiguousarray(S, np.float32)),
                                 _p(out))
+    return out
+
+
+def norms(x_bf16: np.ndarray) -> np.ndarray:
+    """fp16 bits of the encoder's stored norms, [M] (the norm step of encode_mse alone)."""
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    m, d = x.shape
+    out = np.zeros(m, np.uint16)
+    lib().tq_oracle_norms(_p(x), m, d, _p(out))
     return out
 
 

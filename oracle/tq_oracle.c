@@ -253,6 +253,21 @@ void tq_oracle_rotated(const uint16_t* x, int64_t n_vec, int D, const float* R, 
     }
 }
 
+/* fp16 bits of the stored norm of each vector (the encoder's norm step alone):
+ * f16_rne(sqrt(fma chain of x_d^2)), 0 -> 1.  For tests over many vectors. */
+void tq_oracle_norms(const uint16_t* x, int64_t n_vec, int D, uint16_t* norms_out) {
+    for (int64_t v = 0; v < n_vec; ++v) {
+        float ss = 0.0f;
+        for (int d = 0; d < D; ++d) {
+            float f = bf16_to_f32(x[v * D + d]);
+            ss = fmaf(f, f, ss);
+        }
+        float n = sqrtf(ss);
+        if (!(n > 0.0f)) n = 1.0f;
+        norms_out[v] = tq_oracle_f32_to_f16(n);
+    }
+}
+
 /* Bulk conversions (used by tests to pin the rounding helpers against numpy). */
 void tq_oracle_f32_to_f16_array(const float* in, int64_t n, uint16_t* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = tq_oracle_f32_to_f16(in[i]);

@@ -160,3 +160,39 @@ def test_dequantize_prod_matches_oracle(cuda, bits):
                         signs[:, :, :150].cpu().numpy().reshape(300, -1), u16(rnorms[:, :, :150]).reshape(-1),
                         kb, D, R, C, lc.qjl.cpu().numpy())
     assert np.array_equal(u16(out).reshape(300, D), ref)
+
+
+def test_norms_correctly_rounded_over_a_million_vectors(cuda, golden_dir):
+    """Stored norms are fp16(correctly rounded sqrt(fma chain)) for 1M vectors; about one in
+    4000 lands on an fp16 rounding midpoint, where a square root one ulp low (the bare
+    hardware instruction) stores the other neighbour.  Includes a known midpoint row."""
+    tie = torch.from_numpy(np.load(golden_dir / "norm_tie_row.npy").view(np.int16)).view(torch.bfloat16)
+    x = kv_bf16((8, 8, 16384, D), seed=77, device=cuda)
+    x[0, 0, 0] = tie.to(cuda)
+    codec = layer_codecs(D, 4, 0, False, cuda).value
+    codes = torch.empty(8, 8, 16384, 64, dtype=torch.uint8, device=cuda)
+    norms = torch.empty(8, 8, 16384, dtype=torch.float16, device=cuda)
+    K.quantize_mse(x, codec, codes, norms)
+    torch.cuda.synchronize()
+    got = u16(norms).reshape(-1)
+    ref = O.norms(u16(x).reshape(-1, D))
+    assert got[0] == 0x4570
+    assert np.array_equal(got, ref), f"{(got != ref).sum()} of {ref.size} norms differ"
+
+
+def test_residual_norms_correctly_rounded(cuda):
+    """The same for the Q_prod residual norms (32K keys against the full oracle encoder)."""
+    x = kv_bf16((2, 4, 4096, D), seed=78, device=cuda)
+    lc = layer_codecs(D, 4, 0, True, cuda)
+    bufs = [torch.empty(2, 4, 4096, 48, dtype=torch.uint8, device=cuda),
+            torch.empty(2, 4, 4096, dtype=torch.float16, device=cuda),
+            torch.empty(2, 4, 4096, 16, dtype=torch.uint8, device=cuda),
+            torch.empty(2, 4, 4096, dtype=torch.float16, device=cuda)]
+    K.quantize_prod(x, lc.key, lc.qjl, *bufs)
+    torch.cuda.synchronize()
+    R, C, bnd = _host(lc.key)
+    rc, rn, rs, rr = O.encode_prod(u16(x).reshape(-1, D), 3, R, C, bnd, lc.qjl.cpu().numpy())
+    assert np.array_equal(u16(bufs[1]).reshape(-1), rn)
+    assert np.array_equal(u16(bufs[3]).reshape(-1), rr)
+    assert np.array_equal(bufs[0].cpu().numpy().reshape(rc.shape), rc)
+    assert np.array_equal(bufs[2].cpu().numpy().reshape(rs.shape), rs)

@@ -77,6 +77,49 @@ def test_f16_conversion_matches_numpy():
         assert np.array_equal(O.f32_to_f16_bits(arr), arr.astype(np.float16).view(np.uint16))
 
 
+def test_norm_is_correctly_rounded_at_an_fp16_tie(golden_dir):
+    """A bf16 row (from the config-4 generator) whose fp32 norm rounds correctly to exactly
+    the fp16 midpoint 5.435546875, so a sqrt one ulp low stores 0x456F instead of 0x4570.
+    Exact rational arithmetic fixes the expected bits: the fp32 fma chain of squares, the
+    correctly rounded fp32 square root, then fp16 round-to-nearest-even."""
+    from decimal import Decimal, getcontext
+    from fractions import Fraction
+
+    row = np.load(golden_dir / "norm_tie_row.npy")
+
+    def rn32(fr):
+        if fr == 0:
+            return Fraction(0)
+        e = fr.numerator.bit_length() - fr.denominator.bit_length()
+        while Fraction(2) ** e > fr:
+            e -= 1
+        while Fraction(2) ** (e + 1) <= fr:
+            e += 1
+        ulp = Fraction(2) ** (e - 23)
+        q, r = divmod(fr, ulp)
+        if r * 2 > ulp or (r * 2 == ulp and q % 2 == 1):
+            q += 1
+        return q * ulp
+
+    ss = Fraction(0)
+    for v in O.bf16_bits_to_f32(row).astype(np.float64):
+        ss = rn32(Fraction(v) * Fraction(v) + ss)
+    getcontext().prec = 60
+    root = (Decimal(ss.numerator) / Decimal(ss.denominator)).sqrt()
+    n = rn32(Fraction(str(root)))
+    assert n == Fraction(5.435546875)  # an fp16 midpoint, exactly
+    assert np.float16(float(n)).view(np.uint16) == 0x4570  # ties to even
+    assert O.norms(row.reshape(1, -1))[0] == 0x4570
+    assert O.encode_mse(row.reshape(1, -1), 4, np.eye(D, dtype=np.float32), codebook_f32(D, 4)[1])[1][0] == 0x4570
+
+
+def test_norms_function_equals_encoder_norms():
+    rng = np.random.default_rng(4)
+    x = torch.from_numpy(rng.standard_normal((3000, D)).astype(np.float32) * 7).to(torch.bfloat16)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.norms(xb), O.encode_mse(xb, 2, np.eye(D, dtype=np.float32), codebook_f32(D, 2)[1])[1])
+
+
 def test_bf16_conversion_matches_torch():
     rng = np.random.default_rng(1)
     x = (rng.standard_normal(1_000_000) * np.exp(rng.uniform(-30, 30, 1_000_000))).astype(np.float32)

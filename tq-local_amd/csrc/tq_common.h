@@ -33,9 +33,12 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits) {
 }
 
 // IEEE-exact fp32 division and square root (the quantizer is bit-exact against
-// a CPU restatement that uses C's '/' and sqrtf).
-__device__ __forceinline__ float div_rn(float a, float b) { return __fdiv_rn(a, b); }
-__device__ __forceinline__ float sqrt_rn(float a) { return __fsqrt_rn(a); }
+// a CPU restatement that uses C's '/' and sqrtf).  '/' lowers to the full IEEE division
+// sequence; __builtin_sqrtf to v_sqrt_f32 plus a +-1 ulp fma-residual correction, which
+// rounds correctly.  (__fsqrt_rn is the bare v_sqrt_f32 unless the header's rounded-
+// operation switch is set, and is off by one ulp for some inputs.)
+__device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
+__device__ __forceinline__ float sqrt_rn(float a) { return __builtin_sqrtf(a); }
 
 // Bits [pos, pos+n) of a little-endian word array held in registers, pos and
 // n compile-time constants after unrolling: one v_bfe_u32, plus a v_alignbit_b32

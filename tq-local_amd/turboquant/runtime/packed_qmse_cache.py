@@ -168,8 +168,8 @@ class PackedMSELayer(CacheLayerMixin):
         self._shape: tuple[int, int, int] | None = None  # (B, H, D)
         self._force_dense = False
         self._lazy_update = False
-        self._dense_keys: torch.Tensor | None = None
-        self._dense_values: torch.Tensor | None = None
+        self._dense_buf: tuple[torch.Tensor, torch.Tensor] | None = None  # capacity buffers [B, H, cap, D]
+        self._dense_len = 0
 
     # ------------------------------------------------------------- parameters
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
@@ -337,7 +337,7 @@ class PackedMSELayer(CacheLayerMixin):
         """Prefill: compress the whole dense K/V (reference :332-374)."""
         if force_dense:
             self.device, self.dtype = key_states.device, key_states.dtype
-            self._dense_keys, self._dense_values = key_states, value_states
+            self._append_dense(key_states, value_states)
             self._force_dense = True
             self.is_initialized = True
             return
@@ -434,20 +434,39 @@ class PackedMSELayer(CacheLayerMixin):
             self._append_dense(key_states, value_states)
         return key_states, value_states
 
+    @property
+    def _dense_keys(self) -> torch.Tensor | None:
+        """Tokens kept dense (reference attribute): a [:, :, :n] view of the capacity buffer."""
+        return None if self._dense_buf is None else self._dense_buf[0][:, :, :self._dense_len]
+
+    @property
+    def _dense_values(self) -> torch.Tensor | None:
+        return None if self._dense_buf is None else self._dense_buf[1][:, :, :self._dense_len]
+
     def _append_dense(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        if self._dense_keys is None:
-            self._dense_keys, self._dense_values = key_states, value_states
-        else:
-            self._dense_keys = torch.cat((self._dense_keys, key_states), dim=-2)
-            self._dense_values = torch.cat((self._dense_values, value_states), dim=-2)
+        """Append [B, H, T, D] tokens to the dense buffers in place (the reference concatenates
+        the whole history each step, runtime/packed_qmse_cache.py:670-677, 695-702)."""
+        T = int(key_states.shape[-2])
+        n = self._dense_len
+        if self._dense_buf is None or n + T > self._dense_buf[0].shape[2]:
+            cap = max(n + T + self.reserve_tokens, 2 * (0 if self._dense_buf is None else self._dense_buf[0].shape[2]))
+            new = tuple(torch.empty(*x.shape[:2], cap, x.shape[3], dtype=x.dtype, device=x.device)
+                        for x in (key_states, value_states))
+            if self._dense_buf is not None and n:
+                for dst, src in zip(new, self._dense_buf):
+                    dst[:, :, :n].copy_(src[:, :, :n])
+            self._dense_buf = new
+        self._dense_buf[0][:, :, n:n + T].copy_(key_states)
+        self._dense_buf[1][:, :, n:n + T].copy_(value_states)
+        self._dense_len = n + T
 
     def _update_dense_decode(self, key_states: torch.Tensor, value_states: torch.Tensor):
         """Reference :681-705: generated tokens stay dense; history is decoded."""
         pk, pv = self._decode_keys_full(), self._decode_values_full()
         self._append_dense(key_states, value_states)
-        ks = [t for t in (pk, self._dense_keys) if t is not None]
-        vs = [t for t in (pv, self._dense_values) if t is not None]
-        return torch.cat(ks, dim=-2), torch.cat(vs, dim=-2)
+        if pk is None:  # nothing packed (norm-guarded layer): the dense buffers themselves
+            return self._dense_keys, self._dense_values
+        return torch.cat((pk, self._dense_keys), dim=-2), torch.cat((pv, self._dense_values), dim=-2)
 
     def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
         if torch.is_tensor(query_length):  # older callers pass cache_position
