@@ -201,6 +201,114 @@ def bench_split(args, dev) -> dict:
     }
 
 
+class _IdTokenizer:
+    """Bijective id <-> character map over the whole vocabulary (no tokenizer files offline):
+    id i is the code point 0x20000 + i, so decode -> encode returns the same ids."""
+
+    eos_token_id = None
+    pad_token_id = None
+    BASE = 0x20000
+
+    def encode(self, text, add_special_tokens=True):
+        return [ord(c) - self.BASE for c in text]
+
+    def decode(self, ids, skip_special_tokens=True):
+        return "".join(chr(self.BASE + int(i)) for i in ids)
+
+
+def bench_c5(args, dev) -> dict:
+    """a random-init QwQ-32B-architecture model (Qwen2, 64 layers, hidden
+    5120, 40/8 heads, SwiGLU 27648, vocab 152064, rope theta 1e6, bf16) on one GPU; 131072
+    uniform random prompt ids, then 512 greedy tokens with EOS disabled, through
+    turboquant.activate(bits=4, Q_prod keys, quantize_decode=True) and model.generate."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    import turboquant
+    from turboquant.runtime import kernels as K
+    from turboquant.runtime.params import layer_codecs
+    from turboquant.runtime.synthetic import kv_bf16, query_bf16
+
+    prompt, new = args.c5_prompt, args.c5_new
+    cfg = Qwen2Config(vocab_size=152064, hidden_size=5120, intermediate_size=27648, num_hidden_layers=args.c5_layers,
+                      num_attention_heads=40, num_key_value_heads=8, max_position_embeddings=prompt + new,
+                      rope_parameters={"rope_type": "default", "rope_theta": 1e6}, rms_norm_eps=1e-5,
+                      tie_word_embeddings=False)
+    cfg._attn_implementation = "sdpa"
+    t0 = time.perf_counter()
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen2ForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    model.generation_config.eos_token_id = None
+    init_s = time.perf_counter() - t0
+    print(f"[bench] c5 model ready in {init_s:.1f} s ({sum(p.numel() for p in model.parameters()) / 1e9:.2f} B "
+          "parameters)", file=sys.stderr, flush=True)
+    turboquant.activate(model, _IdTokenizer(), bits=4, use_qjl_keys=True, quantize_decode=True, quiet=True)
+    ids = torch.randint(0, cfg.vocab_size, (1, prompt), generator=torch.Generator().manual_seed(5)).to(dev)
+    model.generate(ids[:, :2048], max_new_tokens=4)  # untimed: kernel loading, GEMM heuristics, allocator
+    runs = {}
+    for n_new in (2, new):  # the difference isolates the decode steps from prefill + packing
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        out = model.generate(ids, max_new_tokens=n_new)
+        torch.cuda.synchronize()
+        runs[n_new] = time.perf_counter() - t
+        assert out.shape == (1, prompt + n_new) and torch.equal(out[0, :prompt], ids[0])
+        print(f"[bench] c5 generate {n_new} tokens: {runs[n_new]:.2f} s", file=sys.stderr, flush=True)
+    tel = turboquant.last_telemetry(model)
+    turboquant.deactivate(model, quiet=True)
+    decode_s = runs[new] - runs[2]
+    step_ms = decode_s / (new - 2) * 1e3
+    del model
+    torch.cuda.empty_cache()
+    # the decode attention kernel alone on one packed layer of the final shape (N = prompt + new)
+    N = prompt + new
+    lc = layer_codecs(128, 4, 0, True, dev)
+    k, v = kv_bf16((1, 8, N, 128), seed=1, device=dev), kv_bf16((1, 8, N, 128), seed=2, device=dev)
+    L = {"k_codes": torch.empty(1, 8, N, 48, dtype=torch.uint8, device=dev),
+         "k_norms": torch.empty(1, 8, N, dtype=torch.float16, device=dev),
+         "k_signs": torch.empty(1, 8, N, 16, dtype=torch.uint8, device=dev),
+         "k_rnorms": torch.empty(1, 8, N, dtype=torch.float16, device=dev),
+         "v_codes": torch.empty(1, 8, N, 64, dtype=torch.uint8, device=dev),
+         "v_norms": torch.empty(1, 8, N, dtype=torch.float16, device=dev)}
+    K.quantize_prod(k, lc.key, lc.qjl, L["k_codes"], L["k_norms"], L["k_signs"], L["k_rnorms"])
+    K.quantize_mse(v, lc.value, L["v_codes"], L["v_norms"])
+    q = query_bf16(1, 40, 128, seed=3, device=dev)
+    for _ in range(3):
+        K.decode_attention(q, n_tokens=N, key=lc.key, value=lc.value, qjl=lc.qjl, **L)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        K.decode_attention(q, n_tokens=N, key=lc.key, value=lc.value, qjl=lc.qjl, **L)
+    e1.record()
+    torch.cuda.synchronize()
+    attn_us = e0.elapsed_time(e1) * 1e3 / 20
+    return {
+        "metric": "config 5 end-to-end decode tokens/s (random-init QwQ-32B architecture, 128K prompt)",
+        "value": round((new - 2) / decode_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "vs_baseline": None,
+        "dtype": "bf16 model; u8 packed KV",
+        "data": "synthetic (uniform random ids, random-init weights)",
+        "config": {"workload": f"QwQ-32B architecture, {cfg.num_hidden_layers} layers, prompt {prompt}, "
+                               f"{new} greedy tokens, batch 1, 4-bit Q_prod K / 4-bit Q_mse V, quantize_decode",
+                   "model_init_s": round(init_s, 1)},
+        "decode_ms_per_token": round(step_ms, 3),
+        "prefill_and_pack_s": round(runs[2], 2),
+        "generate_s": round(runs[new], 2),
+        "attention_us_per_layer": round(attn_us, 2),
+        "attention_share_of_decode_step": round(cfg.num_hidden_layers * attn_us * 1e-3 / step_ms, 4),
+        "telemetry": tel,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -220,6 +328,11 @@ def main() -> int:
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--outliers", type=int, default=0,
                     help="measure outlier-split layers with this many outlier channels instead of the C2 line")
+    ap.add_argument("--c5", action="store_true",
+                    help="BASELINE config 5 end to end (random-init QwQ-32B architecture) instead of the C2 line")
+    ap.add_argument("--c5-layers", type=int, default=64)
+    ap.add_argument("--c5-prompt", type=int, default=131072)
+    ap.add_argument("--c5-new", type=int, default=512)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -240,6 +353,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.outliers:
         print(json.dumps(bench_split(args, dev)))
+        return 0
+    if args.c5:
+        print(json.dumps(bench_c5(args, dev)))
         return 0
     B, Hq, Hkv, N, D, bits = args.batch, args.q_heads, args.kv_heads, args.context, 128, args.bits
     qjl = not args.no_qjl
