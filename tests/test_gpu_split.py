@@ -313,3 +313,67 @@ def test_activate_generate_with_outlier_split(cuda):
     per_tok = (47 + 2 + 16 + 2 + 62 + 2) + (2 + 2 + 1 + 2 + 3 + 2)
     assert t["packed_actual_bytes"] == 2 * 2 * 150 * per_tok
     turboquant.deactivate(model, quiet=True)
+
+
+@pytest.mark.parametrize("Hq,Hkv,bits,extra,k,qjl", [
+    (28, 4, 4, 1, 3, True),    # GQA 7 (heads 7 of 8 in the wide kernel)
+    (8, 8, 2, 3, 13, True),    # one query head per KV head
+    (16, 2, 1, 2, 64, False),  # 1-bit normal group, half the channels outliers
+    (12, 4, 3, 5, 5, False),   # 8-bit outlier values
+])
+def test_group_attention_shapes(cuda, Hq, Hkv, bits, extra, k, qjl):
+    """tq_decode_attention_groups against the fp64 formula over the groups across GQA
+    widths, group sizes and bit widths (ragged token count, partial last tile)."""
+    B, N = 2, 777
+    kx = kv_bf16((B, Hkv, N, D), seed=60 + k, device=cuda, outlier_channels=k)
+    vx = kv_bf16((B, Hkv, N, D), seed=61 + k, device=cuda)
+    layer = PackedMSELayer(bits=bits, num_outlier_channels=k, outlier_extra_bits=extra, use_qjl_keys=qjl,
+                           quantize_decode=True)
+    layer.initialize_from_dense(kx, vx)
+    sc = layer._split
+    q = query_bf16(B, Hq, D, seed=62, device=cuda)
+    _, out = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=N, key_stack=sc.key_stack,
+                                       value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, want_f32=True)
+    ref = O.split_fused_attention_f64(u16(q), _host_groups(layer), D)
+    err = np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("bits,qjl", [(5, False), (8, False), (6, True)])
+def test_single_group_attention_at_wide_bit_widths(cuda, bits, qjl):
+    """One group of all 128 channels (n_groups = 1): the unsplit layer at widths the MFMA
+    kernel does not take, against the unsplit fp64 formula."""
+    from turboquant.runtime.params import _group
+
+    B, Hq, Hkv, N = 1, 8, 2, 300
+    ch = np.arange(D, dtype=np.int32)
+    kg = _group(ch, bits - 1 if qjl else bits, 1 if qjl else 0, cuda, 32769, qjl_seed=31337 if qjl else None)
+    vg = _group(ch, bits, 0, cuda, 32769)
+    kx = kv_bf16((B, Hkv, N, D), seed=70 + bits, device=cuda)
+    vx = kv_bf16((B, Hkv, N, D), seed=71 + bits, device=cuda)
+    buf = {"key": kg, "value": vg,
+           "k_codes": torch.zeros(B, Hkv, N, K.row_bytes(D, kg.bits), dtype=torch.uint8, device=cuda),
+           "k_norms": torch.zeros(B, Hkv, N, dtype=torch.float16, device=cuda),
+           "k_signs": torch.zeros(B, Hkv, N, D // 8, dtype=torch.uint8, device=cuda) if qjl else None,
+           "k_rnorms": torch.zeros(B, Hkv, N, dtype=torch.float16, device=cuda) if qjl else None,
+           "v_codes": torch.zeros(B, Hkv, N, K.row_bytes(D, bits), dtype=torch.uint8, device=cuda),
+           "v_norms": torch.zeros(B, Hkv, N, dtype=torch.float16, device=cuda)}
+    K.quantize_group(kx, kg, buf["k_codes"], buf["k_norms"], buf["k_signs"], buf["k_rnorms"])
+    K.quantize_group(vx, vg, buf["v_codes"], buf["v_norms"])
+    q = query_bf16(B, Hq, D, seed=72, device=cuda)
+    _, out = K.decode_attention_groups(q, [buf], n_tokens=N, key_stack=kg.rotation_ch, value_stack=vg.rotation_ch,
+                                       qjl_stack=kg.qjl_ch, want_f32=True)
+    layer = {"kcodes": buf["k_codes"].cpu().numpy(), "knorms": u16(buf["k_norms"]),
+             "vcodes": buf["v_codes"].cpu().numpy(), "vnorms": u16(buf["v_norms"]),
+             "signs": buf["k_signs"].cpu().numpy() if qjl else None, "rnorms": u16(buf["k_rnorms"]) if qjl else None,
+             "Rk": kg.rotation.cpu().numpy(), "Ck": kg.centers.cpu().numpy(), "Rv": vg.rotation.cpu().numpy(),
+             "Cv": vg.centers.cpu().numpy(), "S": kg.qjl.cpu().numpy() if qjl else None, "kbits": kg.bits,
+             "vbits": bits}
+    ref = O.fused_attention_f64(u16(q), layer)
+    err = np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= TOL, err
+    # the codes themselves are the oracle's at D = 128
+    _, _, bv = _host(vg)
+    rc, rn = O.encode_mse(u16(vx).reshape(-1, D), bits, vg.rotation.cpu().numpy(), bv)
+    assert np.array_equal(buf["v_codes"].cpu().numpy().reshape(rc.shape), rc)
+    assert np.array_equal(u16(buf["v_norms"]).reshape(-1), rn)
