@@ -133,6 +133,19 @@ def test_attention_full_length_c2_rows(cuda):
     check(out32, O.fused_attention_f64(u16(q), host_layer(lc, L, N)))
 
 
+def test_attention_full_size_c3(cuda):
+    """BASELINE config 3 at its full shape (B=16, Hq=32, Hkv=8, N=65536, 3-bit Q_mse keys and
+    values, codes straddling bytes and words): rows 0 and 15 against the fp64 oracle."""
+    B, Hq, Hkv, N = 16, 32, 8, 65536
+    lc, L = build_layer(cuda, B, Hkv, N, 3, False, seed=303)
+    q = query_bf16(B, Hq, D, seed=303, device=cuda)
+    _, out32 = run(lc, L, q, N)
+    torch.cuda.synchronize()
+    for b in (0, B - 1):
+        row = host_layer(lc, {k: (None if v is None else v[b:b + 1]) for k, v in L.items()}, N)
+        check(out32[b:b + 1], O.fused_attention_f64(u16(q[b:b + 1]), row))
+
+
 def test_attention_sharp_softmax(cuda):
     """Large key norms make the softmax nearly one-hot (stresses max tracking across splits)."""
     lc, L = build_layer(cuda, 1, 2, 5000, 4, True, seed=9, kv_mu=float(np.log(400.0)))
