@@ -107,6 +107,10 @@ def greedy_decode_with_prefill_cache(*, model, tokenizer, inputs, max_new_tokens
                     if variant == "qmse_packed" else None)
         actual = recon = packed = old_impl = None
         if variant == "qmse_packed":
+            if torch.cuda.is_available():
+                # the prefill kernels are still running: without this wait their tail would be
+                # counted as quantization time at the packing's first host sync
+                torch.cuda.synchronize()
             t0 = time.monotonic()
             packed = build_packed_mse_cache(past, bits=qmse_bits, seed=rotation_seed,
                                             num_outlier_channels=num_outlier_channels,
