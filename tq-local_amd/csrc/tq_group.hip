@@ -213,24 +213,32 @@ __global__ __launch_bounds__(GBLOCK) void dequantize_group_kernel(
 #pragma unroll
     for (int i = 0; i < D / 2; ++i)
         kh[i] = tq::f32_to_bf16(acc[2 * i] * nf) | (tq::f32_to_bf16(acc[2 * i + 1] * nf) << 16);
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i) __asm__("" : "+v"(kh[i]));  // packed here: acc dies before the QJL part
     if constexpr (QJL) {
+        // the correction in two halves of D/2 channels (each channel's fma chain is unchanged)
         const uint8_t* srow = signs + slot * (int64_t)((sub_dim + 7) >> 3);
-#pragma unroll
-        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
-        for (int i = 0; i < sub_dim; ++i) {
-            const float si = ((srow[i >> 3] >> (i & 7)) & 1u) ? 1.0f : -1.0f;
-            const float* Si = S + i * D;
-#pragma unroll
-            for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(si, Si[d], acc[d]);
-        }
         const float rn = tq::f16_to_f32(rnorms[slot]);
 #pragma unroll
-        for (int i = 0; i < D / 2; ++i) {
-            const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((acc[2 * i] * rn) * qs));
-            const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((acc[2 * i + 1] * rn) * qs));
-            const float k0 = tq::bf16_to_f32(kh[i] & 0xFFFFu) + c0;
-            const float k1 = tq::bf16_to_f32(kh[i] >> 16) + c1;
-            kh[i] = tq::f32_to_bf16(k0) | (tq::f32_to_bf16(k1) << 16);
+        for (int half = 0; half < 2; ++half) {
+            float cacc[D / 2];
+#pragma unroll
+            for (int d = 0; d < D / 2; ++d) cacc[d] = 0.0f;
+            for (int i = 0; i < sub_dim; ++i) {
+                const float si = ((srow[i >> 3] >> (i & 7)) & 1u) ? 1.0f : -1.0f;
+                const float* Si = S + i * D + half * (D / 2);
+#pragma unroll
+                for (int d = 0; d < D / 2; ++d) cacc[d] = __builtin_fmaf(si, Si[d], cacc[d]);
+            }
+#pragma unroll
+            for (int i = 0; i < D / 4; ++i) {
+                const int p = half * (D / 4) + i;
+                const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((cacc[2 * i] * rn) * qs));
+                const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((cacc[2 * i + 1] * rn) * qs));
+                const float k0 = tq::bf16_to_f32(kh[p] & 0xFFFFu) + c0;
+                const float k1 = tq::bf16_to_f32(kh[p] >> 16) + c1;
+                kh[p] = tq::f32_to_bf16(k0) | (tq::f32_to_bf16(k1) << 16);
+            }
         }
     }
     uint4* o4 = reinterpret_cast<uint4*>(out + v * D);
