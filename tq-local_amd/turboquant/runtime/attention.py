@@ -3,13 +3,15 @@
 ``turboquant_attention_forward`` is registered under the name "turboquant"
 (reference ``runtime/attention.py:28-120``).  With a packed cache layer on
 the module (``module._tq_cache_layer``) a decode step runs the fused libtq
-kernel over the packed history; without one (prefill, norm-guarded dense
-layers) it is plain SDPA, as in the reference.
+kernel over the packed history, and several query tokens at once run
+``chunked_turboquant_attention`` (libtq decoding, fp32 online softmax); without a
+packed layer (prefill, norm-guarded dense layers) it is plain SDPA, as in the
+reference.
 
 ``fused_attention`` replaces the reference's Triton host wrapper
-(``runtime/triton_kernels.py:238-368``).  Unlike the reference it accepts any
-batch size (one query token per row) and honours left/right padding from the
-attention mask; it has no fallback path -- shapes it does not cover raise.
+(``runtime/triton_kernels.py:238-368``) with its contract (None = not applicable,
+which here means more than one query token).  Unlike the reference it accepts any
+batch size and honours left/right padding from the attention mask.
 
 Outlier-split layers run libtq's channel-group attention kernel
 (``tq_decode_attention_groups``), which scores each channel group in its own
@@ -26,6 +28,7 @@ from typing import TYPE_CHECKING
 import torch
 import torch.nn.functional as F
 
+from turboquant.runtime import _lib
 from turboquant.runtime import kernels as K
 
 if TYPE_CHECKING:
@@ -72,7 +75,7 @@ def _group_buffers(layer: "PackedMSELayer") -> list[dict]:
 
 
 def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", n_kv_groups: int,
-                    attention_mask: torch.Tensor | None = None) -> torch.Tensor:
+                    attention_mask: torch.Tensor | None = None) -> torch.Tensor | None:
     """Decode attention of [B, Hq, 1, D] queries over a packed layer -> [B, Hq, 1, D].
 
     The logit scale is 1/sqrt(D) (reference ``triton_kernels.py:285``).  Tokens
@@ -82,8 +85,7 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
     """
     B, Hq, Sq, D = query_states.shape
     if Sq != 1:
-        raise NotImplementedError("TurboQuant fused attention takes one decode token per sequence "
-                                  f"(got {Sq}); prefill runs dense SDPA before the cache is packed")
+        return None  # the caller takes chunked_turboquant_attention (reference contract)
     store = packed_layer._store
     n_packed = packed_layer.packed_seq_length()
     n_dense = 0 if packed_layer._dense_keys is None else int(packed_layer._dense_keys.shape[-2])
@@ -122,6 +124,80 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
     return (num / den).to(query_states.dtype).view(B, Hq, 1, D)
 
 
+_DEFAULT_CHUNK_SIZE = 1024
+
+
+def triton_available() -> bool:
+    """Reference API (runtime/triton_kernels.py): whether the fused decode kernels are usable.
+    Here that is libtq.so (there is no Triton in this build)."""
+    try:
+        _lib.load()
+    except (ImportError, OSError):
+        return False
+    return True
+
+
+def _repeat_kv(t: torch.Tensor, n_rep: int) -> torch.Tensor:
+    return t if n_rep == 1 else t.repeat_interleave(n_rep, dim=1)
+
+
+def _additive_mask(mask: torch.Tensor | None) -> torch.Tensor | None:
+    if mask is None:
+        return None
+    if mask.dtype == torch.bool:
+        return torch.zeros(mask.shape, dtype=torch.float32, device=mask.device).masked_fill(~mask, float("-inf"))
+    return mask.float()
+
+
+def chunked_turboquant_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer",
+                                 new_key: torch.Tensor | None = None, new_value: torch.Tensor | None = None,
+                                 n_kv_groups: int = 1, attention_mask: torch.Tensor | None = None,
+                                 chunk_size: int = _DEFAULT_CHUNK_SIZE) -> torch.Tensor:
+    """Any-shape attention over a packed layer -> [B, Q, Sq, D] (reference runtime/attention.py:215-304).
+
+    The packed history is decoded by libtq ``chunk_size`` tokens at a time into bf16 K / V
+    rows (reference ``_decode_keys_range`` / ``_decode_values_range``), then the dense decode
+    buffer and ``new_key`` / ``new_value`` follow; logits are fp32 ``q . K / sqrt(D)`` plus
+    the mask slice of each part, merged by an online softmax and normalised with the 1e-8
+    clamp.  A boolean mask (True = attend) is applied as 0 / -inf; the reference adds
+    ``mask.float()``, which is only right for additive masks.  Rows with nothing to attend
+    to return zeros (the reference's running maximum turns them into NaN).
+    """
+    B, Q, Sq, D = query_states.shape
+    scale = 1.0 / math.sqrt(D)
+    qf = query_states.float()
+    mask = _additive_mask(attention_mask)
+    m = torch.full((B, Q, Sq, 1), float("-inf"), device=qf.device)
+    s = torch.zeros(B, Q, Sq, 1, device=qf.device)
+    o = torch.zeros(B, Q, Sq, D, device=qf.device)
+    off = 0
+
+    def attend(keys: torch.Tensor, values: torch.Tensor) -> None:
+        nonlocal m, s, o, off
+        n = int(keys.shape[-2])
+        logits = (qf @ _repeat_kv(keys, n_kv_groups).float().transpose(-2, -1)) * scale
+        if mask is not None:
+            logits = logits + mask[..., off:off + n]
+        new_m = torch.maximum(m, logits.amax(dim=-1, keepdim=True))
+        safe = torch.where(torch.isfinite(new_m), new_m, torch.zeros_like(new_m))
+        corr = torch.exp(m - safe)
+        e = torch.exp(logits - safe)
+        s = s * corr + e.sum(dim=-1, keepdim=True)
+        o = o * corr + e @ _repeat_kv(values, n_kv_groups).float()
+        m = new_m
+        off += n
+
+    n_packed = packed_layer.packed_seq_length()
+    for a in range(0, n_packed, chunk_size):
+        b = min(a + chunk_size, n_packed)
+        attend(packed_layer._decode_keys_range(a, b), packed_layer._decode_values_range(a, b))
+    if packed_layer._dense_keys is not None:
+        attend(packed_layer._dense_keys, packed_layer._dense_values)
+    if new_key is not None:
+        attend(new_key, new_value)
+    return (o / s.clamp(min=1e-8)).to(query_states.dtype)
+
+
 def _sdpa_fallback(module, query, key, value, attention_mask, scaling):
     """Standard SDPA for prefill and norm-guarded dense layers (reference :75-99)."""
     causal = attention_mask is None and query.shape[-2] > 1
@@ -138,7 +214,11 @@ def turboquant_attention_forward(module: torch.nn.Module, query: torch.Tensor, k
     layer = getattr(module, "_tq_cache_layer", None)
     if layer is None or layer._force_dense or layer.packed_seq_length() == 0:
         return _sdpa_fallback(module, query, key, value, attention_mask, scaling)
-    out = fused_attention(query, layer, getattr(module, "num_key_value_groups", 1), attention_mask)
+    n_kv_groups = getattr(module, "num_key_value_groups", 1)
+    if query.shape[-2] == 1:
+        out = fused_attention(query, layer, n_kv_groups, attention_mask)
+    else:  # several query tokens against the packed history: the reference's chunked path
+        out = chunked_turboquant_attention(query, layer, n_kv_groups=n_kv_groups, attention_mask=attention_mask)
     return out.transpose(1, 2).contiguous(), None
 
 

@@ -36,6 +36,11 @@ def _vp(t: torch.Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _at_slot(t: torch.Tensor | None, start: int):
+    """Pointer to token slot ``start`` of a [B, H, cap, ...] buffer (the group stride stays cap)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr() + start * t.stride(2) * t.element_size())
+
+
 def _stream(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
@@ -168,10 +173,11 @@ def quantize_group(x: torch.Tensor, g: GroupCodec, codes: torch.Tensor, norms: t
 
 
 def dequantize_group(codes: torch.Tensor, norms: torch.Tensor, tokens: int, g: GroupCodec, out: torch.Tensor,
-                     merge: bool, signs: torch.Tensor | None = None, rnorms: torch.Tensor | None = None) -> None:
-    """Decode channel group ``g`` of codes [B,H,cap,row] into out bf16 [B,H,tokens,D] (its
-    channels; the others are zeroed, or kept when ``merge``).  QJL-corrected when ``g``
-    is a Q_prod key group."""
+                     merge: bool, signs: torch.Tensor | None = None, rnorms: torch.Tensor | None = None,
+                     start: int = 0) -> None:
+    """Decode channel group ``g`` of slots [start, start + tokens) of codes [B,H,cap,row] into
+    out bf16 [B,H,tokens,D] (its channels; the others are zeroed, or kept when ``merge``).
+    QJL-corrected when ``g`` is a Q_prod key group."""
     _require_gpu(codes, norms, out, signs, rnorms)
     B, H, cap, _ = codes.shape
     qjl = g.qjl_ch is not None
@@ -179,30 +185,41 @@ def dequantize_group(codes: torch.Tensor, norms: torch.Tensor, tokens: int, g: G
         raise ValueError("a Q_prod key group needs its signs and rnorms")
     if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.shape[:3] != (B, H, tokens):
         raise ValueError("out must be a contiguous bf16 [B, H, tokens, D] tensor")
-    _lib.call("tq_dequantize_group", _vp(codes), _vp(norms), _vp(signs if qjl else None),
-              _vp(rnorms if qjl else None), B * H, tokens, cap, out.shape[-1], g.channels.ctypes.data, g.dim,
+    if start < 0 or start + tokens > cap:
+        raise ValueError(f"slots [{start}, {start + tokens}) outside the capacity {cap}")
+    _lib.call("tq_dequantize_group", _at_slot(codes, start), _at_slot(norms, start),
+              _at_slot(signs if qjl else None, start), _at_slot(rnorms if qjl else None, start), B * H, tokens,
+              cap, out.shape[-1], g.channels.ctypes.data, g.dim,
               g.bits, _vp(g.rotation_ch), _vp(g.centers), _vp(g.qjl_ch), int(bool(merge)), _vp(out),
               _stream(codes.device))
 
 
 def dequantize_mse(codes: torch.Tensor, norms: torch.Tensor, tokens: int, codec: CodecParams,
-                   dim: int = HEAD_DIM) -> torch.Tensor:
-    """codes [B,H,cap,row] -> bf16 [B,H,tokens,D] = bf16((C[codes] @ R) * norm)."""
+                   dim: int = HEAD_DIM, start: int = 0) -> torch.Tensor:
+    """Slots [start, start + tokens) of codes [B,H,cap,row] -> bf16 [B,H,tokens,D] =
+    bf16((C[codes] @ R) * norm)."""
     _require_gpu(codes, norms)
     B, H, cap, _ = codes.shape
+    if start < 0 or start + tokens > cap:
+        raise ValueError(f"slots [{start}, {start + tokens}) outside the capacity {cap}")
     out = torch.empty(B, H, tokens, dim, dtype=torch.bfloat16, device=codes.device)
-    _lib.call("tq_dequantize_mse", _vp(codes), _vp(norms), B * H, tokens, cap, dim, codec.bits,
+    _lib.call("tq_dequantize_mse", _at_slot(codes, start), _at_slot(norms, start), B * H, tokens, cap, dim, codec.bits,
               _vp(codec.rotation), _vp(codec.centers), _vp(out), _stream(codes.device))
     return out
 
 
 def dequantize_prod(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Tensor, rnorms: torch.Tensor,
-                    tokens: int, codec: CodecParams, qjl: torch.Tensor, dim: int = HEAD_DIM) -> torch.Tensor:
-    """Q_prod keys [B,H,cap,...] -> bf16 [B,H,tokens,D]: MSE reconstruction + QJL correction."""
+                    tokens: int, codec: CodecParams, qjl: torch.Tensor, dim: int = HEAD_DIM,
+                    start: int = 0) -> torch.Tensor:
+    """Slots [start, start + tokens) of Q_prod keys [B,H,cap,...] -> bf16 [B,H,tokens,D]:
+    MSE reconstruction + QJL correction."""
     _require_gpu(codes, norms, signs, rnorms)
     B, H, cap, _ = codes.shape
+    if start < 0 or start + tokens > cap:
+        raise ValueError(f"slots [{start}, {start + tokens}) outside the capacity {cap}")
     out = torch.empty(B, H, tokens, dim, dtype=torch.bfloat16, device=codes.device)
-    _lib.call("tq_dequantize_prod", _vp(codes), _vp(norms), _vp(signs), _vp(rnorms), B * H, tokens, cap, dim,
+    _lib.call("tq_dequantize_prod", _at_slot(codes, start), _at_slot(norms, start), _at_slot(signs, start),
+              _at_slot(rnorms, start), B * H, tokens, cap, dim,
               codec.bits, _vp(codec.rotation), _vp(codec.centers), _vp(qjl), _vp(out), _stream(codes.device))
     return out
 

@@ -375,37 +375,42 @@ class PackedMSELayer(CacheLayerMixin):
         s.length += T
 
     # ------------------------------------------------------------- decoding
-    def _decode_split(self, pre: str, normal, outlier) -> torch.Tensor:
-        """Both channel groups decoded into one [B, H, N, D] bf16 tensor (reference
-        _decode_merge / _decode_keys_merge_qjl, :456-515)."""
+    def _decode_split(self, pre: str, normal, outlier, start: int, end: int) -> torch.Tensor:
+        """Both channel groups of slots [start, end) decoded into one [B, H, end - start, D]
+        bf16 tensor (reference _decode_merge / _decode_keys_merge_qjl, :456-515)."""
         s = self._store
         B, H, D = self._shape
-        out = torch.empty(B, H, s.length, D, dtype=torch.bfloat16, device=s.device)
+        out = torch.empty(B, H, end - start, D, dtype=torch.bfloat16, device=s.device)
         qjl = pre == "k" and self.use_qjl_keys
         for sfx, g, merge in (("", normal, False), ("o", outlier, True)):
-            K.dequantize_group(getattr(s, pre + "c" + sfx), getattr(s, pre + "n" + sfx), s.length, g, out, merge,
+            K.dequantize_group(getattr(s, pre + "c" + sfx), getattr(s, pre + "n" + sfx), end - start, g, out, merge,
                                signs=getattr(s, "ks" + sfx) if qjl else None,
-                               rnorms=getattr(s, "kr" + sfx) if qjl else None)
+                               rnorms=getattr(s, "kr" + sfx) if qjl else None, start=start)
         return out
 
-    def _decode_keys_full(self) -> torch.Tensor | None:
+    def _decode_keys_range(self, start: int, end: int) -> torch.Tensor:
+        """Keys of packed positions [start, end) (reference :564-584)."""
         s = self._store
-        if s is None:
-            return None
         if self._split is not None:
-            return self._decode_split("k", self._split.key_normal, self._split.key_outlier).to(self.dtype)
+            return self._decode_split("k", self._split.key_normal, self._split.key_outlier, start, end).to(self.dtype)
         c = self.codecs
         if c.use_qjl_keys:
-            return K.dequantize_prod(s.kc, s.kn, s.ks, s.kr, s.length, c.key, c.qjl).to(self.dtype)
-        return K.dequantize_mse(s.kc, s.kn, s.length, c.key).to(self.dtype)
+            return K.dequantize_prod(s.kc, s.kn, s.ks, s.kr, end - start, c.key, c.qjl, start=start).to(self.dtype)
+        return K.dequantize_mse(s.kc, s.kn, end - start, c.key, start=start).to(self.dtype)
+
+    def _decode_values_range(self, start: int, end: int) -> torch.Tensor:
+        """Values of packed positions [start, end) (reference :586-592)."""
+        s = self._store
+        if self._split is not None:
+            return self._decode_split("v", self._split.value_normal, self._split.value_outlier, start,
+                                      end).to(self.dtype)
+        return K.dequantize_mse(s.vc, s.vn, end - start, self.codecs.value, start=start).to(self.dtype)
+
+    def _decode_keys_full(self) -> torch.Tensor | None:
+        return None if self._store is None else self._decode_keys_range(0, self._store.length)
 
     def _decode_values_full(self) -> torch.Tensor | None:
-        s = self._store
-        if s is None:
-            return None
-        if self._split is not None:
-            return self._decode_split("v", self._split.value_normal, self._split.value_outlier).to(self.dtype)
-        return K.dequantize_mse(s.vc, s.vn, s.length, self.codecs.value).to(self.dtype)
+        return None if self._store is None else self._decode_values_range(0, self._store.length)
 
     # ------------------------------------------------------------ HF protocol
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args: Any,
