@@ -36,6 +36,16 @@ for p in (ROOT / "tq-local_amd", ROOT):
 HBM_PEAK_GBS = 8000.0
 VALU_FP32_PEAK_TFLOPS = 157.3
 
+# BASELINE decode-attention shapes (B, Hq, Hkv, N, bits, qjl) -> the configuration they are
+_SHAPES = {(8, 32, 8, 32768, 4, True): "BASELINE config 2",
+           (16, 32, 8, 65536, 3, False): "BASELINE config 3 shape",
+           (4, 28, 4, 32768, 4, True): "BASELINE config 4 shape",
+           (1, 40, 8, 131584, 4, True): "BASELINE config 5 shape"}
+
+
+def _shape_name(B, Hq, Hkv, N, bits, qjl):
+    return _SHAPES.get((B, Hq, Hkv, N, bits, qjl), "custom shape")
+
 
 def packed_bytes_per_token_head(dim: int, bits: int, qjl: bool) -> int:
     kb = bits - 1 if qjl else bits
@@ -497,7 +507,8 @@ def main() -> int:
         "dtype": "u8 codes; bf16 hi/lo + int8 MFMA, fp32 accumulate",
         "data": "synthetic",
         "config": {
-            "workload": (f"BASELINE config 2: decode attention over {args.layers} independently seeded packed "
+            "workload": (f"{_shape_name(B, Hq, Hkv, N, bits, qjl)}: decode attention over {args.layers} "
+                         f"independently seeded packed "
                          f"layers, B={B}, Hq={Hq}, Hkv={Hkv}, D={D}, N={N}, "
                          + (f"{bits}-bit Q_prod K ({bits - 1}-bit MSE + 1-bit QJL) / {bits}-bit Q_mse V" if qjl
                             else f"{bits}-bit Q_mse K and V")),
