@@ -291,6 +291,9 @@ __device__ __forceinline__ void merge_head(int bh, bool act, int t, int n_split,
     const int d = t & (D - 1), hf = t >> 7;
     float o = 0.0f, sacc = 0.0f;
     if (act && M != NEG_INF) {
+        // unrolled so that several splits' loads are in flight together (the fma order is
+        // unchanged)
+#pragma unroll 4
         for (int k = hf; k < n_split; k += 2) {
             const float mk = ml[2 * k];
             const float e = mk == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
