@@ -608,7 +608,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     };
 
     // ------------------------------------------------------------ prologue
-    // round 1: codebooks (hi|lo) and the group's q-side image (every split workgroup of the
+    // phase 1: codebooks (hi|lo) and the group's q-side image (every split workgroup of the
     // group computes it: two 128 x 128 mat-vecs per head from L2-resident R_k and S, cheaper
     // than a separate launch ahead of the split pass)
     if (tid < (1 << KB)) sm.u.pro.ksrc[tid] = pack_hilo(Ck[tid]);
@@ -618,7 +618,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // zero slots of the weight transpose (never written by the loop)
     for (int i = tid; i < NW * 16 * Sm::WTS; i += NT) (&sm.wt[0][0][0])[i] = 0u;
     __syncthreads();
-    // round 2 (LDS only): pair tables expanded from the codebooks; operands into registers
+    // phase 2 (LDS only): pair tables expanded from the codebooks; operands into registers
     for (int i = tid; i < (1 << (2 * KB)) * Sm::KC; i += NT) {
         const int e = i / Sm::KC;
         (&sm.ktab[0][0])[i] = make_uint2(sm.u.pro.ksrc[e & ((1 << KB) - 1)], sm.u.pro.ksrc[e >> KB]);
