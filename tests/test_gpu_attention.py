@@ -174,7 +174,9 @@ def test_attention_on_reference_golden_layer(cuda, golden_dir):
         ref = O.fused_attention_f64(g[f"{name}_q_bf16"][:, :, 0, :], host_layer(lc, L, n))
         check(out32, ref)
         chunked = O.bf16_bits_to_f32(g[f"{name}_out_bf16"][:, :, 0, :]).astype(np.float64)
-        assert np.abs(out32.cpu().numpy() - chunked).max() <= 2e-2 * np.abs(chunked).max()
+        # the fp64 formula's own gap to this output is 1.485e-2 (prod4) / 4.79e-3 (mse3)
+        bound = {"prod4": 1.6e-2, "mse3": 5.5e-3}[name]
+        assert np.abs(out32.cpu().numpy() - chunked).max() <= bound * np.abs(chunked).max()
 
 
 def test_graph_replay_matches_eager(cuda):

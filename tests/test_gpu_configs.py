@@ -95,9 +95,13 @@ def test_c4_norm_guard_decode_append_and_attention(cuda):
     assert np.array_equal(s.vc[:, :, N:N + STEPS].cpu().numpy().reshape(vc.shape), vc)
     assert np.array_equal(u16(s.vn[:, :, N:N + STEPS]).reshape(-1), vn)
     # attention over the final 33,024-token cache of batch row 3 (GQA 7) against the fp64 formula
-    got = fused_attention(q.float(), layer, HQ // HKV)  # fp32 query: fp32 result of the bf16-rounded kernel
+    got = fused_attention(q.float(), layer, HQ // HKV)  # fp32 query: the kernel's fp32 output
+    assert got.dtype == torch.float32
     ref = O.fused_attention_f64(u16(q[3:4, :, 0]), _host_layer(layer, 3))
     err = np.abs(got[3:4, :, 0].cpu().numpy() - ref).max() / np.abs(ref).max()
-    assert err <= TOL + 2 ** -8, err
+    assert err <= TOL, err
+    # the bf16 result of a bf16 query is the RNE rounding of that fp32 output
+    got16 = fused_attention(q, layer, HQ // HKV)
+    assert np.array_equal(u16(got16), O.f32_to_bf16_bits(got.cpu().numpy()))
     # dense layers attend through SDPA in the model; their cache holds the raw tokens
     assert torch.equal(cache.layers[0]._dense_keys[:, :, N:], new[0][0])

@@ -239,10 +239,14 @@ def test_split_layer_prefill_append_and_attention(cuda, qjl, bits, Hq):
     # the reference's own strategy for split layers (bf16 K^ / V^ rows, exact softmax) lies
     # within the bf16-rounding band of the formula
     assert np.abs(O.dense_attention_f64(u16(q), kh, vh) - ref).max() <= 3e-2 * np.abs(ref).max()
-    # through the attention backend: bf16 out
+    # through the attention backend: an fp32 query gets the fp32 output (held to the
+    # contract), a bf16 query its RNE rounding
+    of = fused_attention(q.float().unsqueeze(2), layer, Hq // Hkv)
+    assert of.dtype == torch.float32
+    assert np.abs(of[:, :, 0].cpu().numpy() - ref).max() <= TOL * np.abs(ref).max()
     ob = fused_attention(q.unsqueeze(2), layer, Hq // Hkv)
     assert ob.dtype == torch.bfloat16
-    assert np.abs(ob[:, :, 0].float().cpu().numpy() - ref).max() <= (TOL + 2 ** -8) * np.abs(ref).max()
+    assert np.array_equal(u16(ob), O.f32_to_bf16_bits(of.cpu().numpy()))
 
 
 def test_split_layer_dense_buffer_and_left_padding(cuda):

@@ -265,6 +265,10 @@ def test_fused_formula_equals_explicit_dequant(att, name):
     assert np.abs(f - d).max() <= 1e-12 * np.abs(f).max()
 
 
+#: max |fused formula - reference chunked output| / ||out||_inf on the golden layers
+CHUNKED_GAP = {"prod4": 1.6e-2, "mse3": 5.5e-3}
+
+
 @pytest.mark.parametrize("name", ["prod4", "mse3"])
 def test_fused_formula_vs_reference_chunked_output(att, name):
     """The reference's CPU chunked path rounds dequantised K and V to bf16 (and the
@@ -274,7 +278,9 @@ def test_fused_formula_vs_reference_chunked_output(att, name):
     layer, q, g = _golden_layer(att, name)
     chunked = O.bf16_bits_to_f32(att[f"{name}_out_bf16"][:, :, 0, :]).astype(np.float64)
     f = O.fused_attention_f64(q, layer)
-    assert np.abs(f - chunked).max() <= 3e-2 * np.abs(f).max()
+    # measured gap: 1.485e-2 (prod4: bf16 K^ carries the rounded QJL correction too) and
+    # 4.79e-3 (mse3) of ||out||_inf; the bounds sit just above
+    assert np.abs(f - chunked).max() <= CHUNKED_GAP[name] * np.abs(f).max()
     P = {"Rk": torch.from_numpy(layer["Rk"]), "Ck": torch.from_numpy(layer["Ck"]),
          "Rv": torch.from_numpy(layer["Rv"]), "Cv": torch.from_numpy(layer["Cv"]),
          "S": None if layer["S"] is None else torch.from_numpy(layer["S"])}

@@ -10,8 +10,10 @@ reference.
 
 ``fused_attention`` replaces the reference's Triton host wrapper
 (``runtime/triton_kernels.py:238-368``) with its contract (None = not applicable,
-which here means more than one query token).  Unlike the reference it accepts any
-batch size and honours left/right padding from the attention mask.
+which here means more than one query token, a GQA group wider than 8 query heads
+per KV head, or a mask whose attended slots are not contiguous).  Unlike the
+reference it accepts any batch size and honours left padding (and right padding
+before the packed history ends) from the attention mask.
 
 Outlier-split layers run libtq's channel-group attention kernel
 (``tq_decode_attention_groups``), which scores each channel group in its own
@@ -35,16 +37,10 @@ if TYPE_CHECKING:
     from turboquant.runtime.packed_qmse_cache import PackedMSELayer
 
 
-def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device):
-    """First / one-past-last attended slot per row from an HF decode mask.
+def _attend_mask(attention_mask: torch.Tensor, B: int, total: int) -> torch.Tensor:
+    """The decode row of an HF mask as bool [B, total] (True = attend).
 
-    The mask is [B, 1, Sq, kv] (bool: True = attend, or additive float) or
-    [B, kv].  Returns (starts, ends) int32 tensors on the device, or (None, None)
-    when no mask is given.  Attended slots are assumed contiguous (padding only at
-    the ends), which holds for left- or right-padded batched generation.
-    """
-    if attention_mask is None:
-        return None, None
+    The mask is [B, 1, Sq, kv] (bool, or additive float) or [B, kv]."""
     m = attention_mask
     if m.dim() == 4:
         m = m[:, 0, -1, :]
@@ -53,12 +49,33 @@ def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device
     m = m[:, :total]
     if m.shape[0] == 1 and B > 1:
         m = m.expand(B, -1)
+    return m
+
+
+def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device, check_contiguous: bool = True):
+    """Per-row attended slot range [start, end) from an HF decode mask.
+
+    Returns (starts, ends) int32 device tensors, or (None, None) without a mask.  The
+    kernel attends to every slot of the range, so a row whose attended slots have a
+    hole (right padding followed by generated tokens) cannot take this path: with
+    ``check_contiguous`` such masks raise ``_HoleyMask`` (one host sync to find out);
+    callers that know the mask's shape pass False.
+    """
+    if attention_mask is None:
+        return None, None
+    m = _attend_mask(attention_mask, B, total)
     idx = torch.arange(m.shape[1], device=m.device, dtype=torch.int32)
     big = torch.iinfo(torch.int32).max
     starts = torch.where(m, idx, torch.full_like(idx, big)).amin(dim=1)
     ends = torch.where(m, idx + 1, torch.zeros_like(idx)).amax(dim=1)
     starts = torch.minimum(starts, ends)
+    if check_contiguous and bool(((ends - starts) != m.sum(dim=1, dtype=torch.int32)).any()):
+        raise _HoleyMask
     return starts.to(device=device, dtype=torch.int32), ends.to(device=device, dtype=torch.int32)
+
+
+class _HoleyMask(Exception):
+    """A decode mask whose attended slots are not one contiguous range per row."""
 
 
 def _group_buffers(layer: "PackedMSELayer") -> list[dict]:
@@ -81,18 +98,36 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
     The logit scale is 1/sqrt(D) (reference ``triton_kernels.py:285``).  Tokens
     kept dense (``quantize_decode=False``) are merged by log-sum-exp.  Outlier-split
     layers go through the channel-group kernel (where the reference returns None and
-    its caller takes the chunked path).
+    its caller takes the chunked path).  The result has the query's dtype; an fp32
+    query gets the kernel's fp32 output (no bf16 rounding).
+
+    Returns None (the reference's "not applicable": the caller takes
+    ``chunked_turboquant_attention``) for several query tokens, for GQA groups wider
+    than the kernels' 8 query heads per KV head, and for a mask whose attended slots are
+    not one contiguous range per row.  The cache layer's ``_tq_mask_contiguous`` (set by
+    the generation loop from the prompt mask) spares the host sync of that last check.
     """
     B, Hq, Sq, D = query_states.shape
     if Sq != 1:
         return None  # the caller takes chunked_turboquant_attention (reference contract)
     store = packed_layer._store
+    Hkv = store.kc.shape[1] if store is not None else Hq // max(n_kv_groups, 1)
+    if Hq // Hkv > K.MAX_GROUP:
+        return None
     n_packed = packed_layer.packed_seq_length()
     n_dense = 0 if packed_layer._dense_keys is None else int(packed_layer._dense_keys.shape[-2])
     scale = 1.0 / math.sqrt(D)
-    starts, ends = _valid_range(attention_mask, B, n_packed + n_dense, query_states.device)
+    known = getattr(packed_layer, "_tq_mask_contiguous", None)
+    if attention_mask is not None and known is False:
+        return None
+    try:
+        starts, ends = _valid_range(attention_mask, B, n_packed + n_dense, query_states.device,
+                                    check_contiguous=known is None)
+    except _HoleyMask:
+        return None
     p_ends = None if ends is None else torch.clamp(ends, max=n_packed)
-    kw = dict(n_tokens=n_packed, seq_starts=starts, seq_lens=p_ends, scale=scale, want_f32=n_dense > 0,
+    f32 = query_states.dtype == torch.float32
+    kw = dict(n_tokens=n_packed, seq_starts=starts, seq_lens=p_ends, scale=scale, want_f32=f32 or n_dense > 0,
               want_lse=n_dense > 0)
     if packed_layer._outlier_enabled:
         sc = packed_layer._split
@@ -104,7 +139,8 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
                                   v_norms=store.vn, key=c.key, value=c.value, k_signs=store.ks, k_rnorms=store.kr,
                                   qjl=c.qjl, **kw)
     if n_dense == 0:
-        return outs.to(query_states.dtype).view(B, Hq, 1, D)
+        out = outs[1] if f32 else outs
+        return out.to(query_states.dtype).view(B, Hq, 1, D)
     _, o_packed, lse_packed = outs
     # dense decode buffer: exact attention on the few generated tokens, merged by LSE
     dk = packed_layer._dense_keys.float().repeat_interleave(n_kv_groups, dim=1)  # [B, Hq, n, D]
@@ -215,9 +251,8 @@ def turboquant_attention_forward(module: torch.nn.Module, query: torch.Tensor, k
     if layer is None or layer._force_dense or layer.packed_seq_length() == 0:
         return _sdpa_fallback(module, query, key, value, attention_mask, scaling)
     n_kv_groups = getattr(module, "num_key_value_groups", 1)
-    if query.shape[-2] == 1:
-        out = fused_attention(query, layer, n_kv_groups, attention_mask)
-    else:  # several query tokens against the packed history: the reference's chunked path
+    out = fused_attention(query, layer, n_kv_groups, attention_mask) if query.shape[-2] == 1 else None
+    if out is None:  # several query tokens, or a shape / mask the fused kernel does not take
         out = chunked_turboquant_attention(query, layer, n_kv_groups=n_kv_groups, attention_mask=attention_mask)
     return out.transpose(1, 2).contiguous(), None
 

@@ -6,6 +6,8 @@ Same inputs, outputs and metrics as the reference.  Differences:
   same, without materialising [B, prompt, vocab] logits;
 * decode steps with the packed cache run the fused libtq kernel for every batch
   size (the reference's fused path is batch-1 only);
+* a prompt mask without padding is dropped for the decode steps, and one look at it
+  tells the attention backend whether every row's attended slots stay contiguous;
 * the research "qmse" fake-quantisation variant is not provided.
 """
 
@@ -130,6 +132,18 @@ def greedy_decode_with_prefill_cache(*, model, tokenizer, inputs, max_new_tokens
             torch.cuda.empty_cache()
         generated = [next_token]
         mask = inputs.get("attention_mask")
+        if mask is not None:
+            # One look at the prompt mask decides the decode masks of the whole call: with no
+            # padding the decode steps need none (nothing to range-check per layer and step);
+            # the fused kernel takes one attended range per row, so right padding (a hole once
+            # generated tokens follow) sends those layers to the chunked path instead.
+            attend = mask.bool()
+            hole = bool(((attend.cumsum(dim=-1) > 0) & ~attend).any())
+            if packed is not None:
+                for layer in packed.layers:
+                    layer._tq_mask_contiguous = not hole
+            if bool(attend.all()):
+                mask = None
         post_setup = gpu_current_memory_bytes()
         if torch.cuda.is_available():
             torch.cuda.reset_peak_memory_stats()

@@ -30,6 +30,7 @@ import torch
 from turboquant.runtime import _lib
 
 HEAD_DIM = 128
+MAX_GROUP = 8  # query heads per KV head the decode-attention kernels take (TQ_MAX_GROUP)
 
 
 def _vp(t: torch.Tensor | None):
@@ -224,16 +225,30 @@ def dequantize_prod(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Tenso
     return out
 
 
+#: partials workspace per (device, stream): calls on one stream are ordered, so they can
+#: share one; calls on two streams get two
 _workspaces: dict[tuple, torch.Tensor] = {}
+#: workspaces replaced by a larger one stay allocated: a HIP graph that captured a call keeps
+#: the old pointer and may be replayed later
+_retired: list[torch.Tensor] = []
+_ws_bytes: dict[tuple, int] = {}
 
 
 def attention_workspace(device: torch.device, batch: int, q_heads: int, kv_heads: int, max_tokens: int) -> torch.Tensor:
-    need = int(_lib.load().tq_decode_attention_workspace_bytes(batch, q_heads, kv_heads, HEAD_DIM, max_tokens))
-    if need == 0:
-        raise ValueError("invalid attention shape for workspace sizing")
-    key = (device.type, device.index)
+    """The partials workspace of ``tq_decode_attention`` for the current stream of ``device``."""
+    shape = (batch, q_heads, kv_heads)
+    need = _ws_bytes.get(shape)
+    if need is None:
+        # sized for any token count (the split count is bounded by the workgroup cap)
+        need = int(_lib.load().tq_decode_attention_workspace_bytes(batch, q_heads, kv_heads, HEAD_DIM, 1))
+        if need == 0:
+            raise ValueError("invalid attention shape for workspace sizing")
+        _ws_bytes[shape] = need
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:
+        if ws is not None:
+            _retired.append(ws)
         ws = torch.empty(need, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
