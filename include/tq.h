@@ -116,6 +116,32 @@ int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * tq_decode_attention without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The per-split partials live in a library-owned device array of
+ * TQ_NOALLOC_SCRATCH_BYTES, one per GPU, held until the process ends; the caller still
+ * passes q, the packed cache and the outputs.  A call whose partials ((dim + 2) fp32 per
+ * query head and split) do not fit is rejected with TQ_ERR_WORKSPACE before anything is
+ * launched; every shape with batch * q_heads * ceil(1024 / (batch * kv_heads)) <= 16000
+ * fits.  All calls on one GPU share its
+ * array: calls that overlap in time on one GPU (on different streams, or from several
+ * host threads) race and must be ordered by the caller.  Nothing needs clearing
+ * between calls (every partial is written before it is read).  Arguments and results
+ * are those of tq_decode_attention.
+ */
+#define TQ_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int tq_decode_attention_noalloc(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
+                                const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
+                                const uint8_t* k_codes, const uint16_t* k_norms,
+                                const uint8_t* k_signs, const uint16_t* k_rnorms,
+                                const uint8_t* v_codes, const uint16_t* v_norms,
+                                int key_bits, int value_bits, int has_qjl,
+                                const float* key_rotation, const float* key_centers, const float* qjl,
+                                const float* value_rotation, const float* value_centers,
+                                float scale, float* out_f32, uint16_t* out_bf16, float* lse_out, void* stream);
+
+/*
  * Dequantise packed Q_mse rows to bf16 (verification / dense fallback of the
  * caller).  Replaces reference _decode_group (runtime/packed_qmse_cache.py:404-435)
  * and triton_decode_group (runtime/triton_kernels.py:227-236):

@@ -42,6 +42,7 @@
 
 #include "tq_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -1359,14 +1360,17 @@ extern "C" size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, in
     return ws_layout(batch, q_heads, bound).total;
 }
 
-extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
-                                   const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
-                                   const uint8_t* k_codes, const uint16_t* k_norms, const uint8_t* k_signs,
-                                   const uint16_t* k_rnorms, const uint8_t* v_codes, const uint16_t* v_norms,
-                                   int key_bits, int value_bits, int has_qjl, const float* key_rotation,
-                                   const float* key_centers, const float* qjl, const float* value_rotation,
-                                   const float* value_centers, float scale, float* out_f32, uint16_t* out_bf16,
-                                   float* lse_out, void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+// The body of tq_decode_attention and tq_decode_attention_noalloc: validation, split sizing,
+// the split pass and the merge, with the partials at `workspace`.
+int decode_attention_impl(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
+                          const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
+                          const uint8_t* k_codes, const uint16_t* k_norms, const uint8_t* k_signs,
+                          const uint16_t* k_rnorms, const uint8_t* v_codes, const uint16_t* v_norms, int key_bits,
+                          int value_bits, int has_qjl, const float* key_rotation, const float* key_centers,
+                          const float* qjl, const float* value_rotation, const float* value_centers, float scale,
+                          float* out_f32, uint16_t* out_bf16, float* lse_out, void* workspace,
+                          size_t workspace_bytes, void* stream) {
     if (!q || batch <= 0 || q_heads <= 0 || kv_heads <= 0 || n_tokens < 0 || cap < n_tokens)
         return TQ_ERR_INVALID_ARGUMENT;
     if (dim != D) return TQ_ERR_UNSUPPORTED;
@@ -1410,6 +1414,67 @@ extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, in
                        out_f32, out_bf16, lse_out);
     TQ_CHECK_LAUNCH();
     return TQ_OK;
+}
+}  // namespace
+
+extern "C" int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
+                                   const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
+                                   const uint8_t* k_codes, const uint16_t* k_norms, const uint8_t* k_signs,
+                                   const uint16_t* k_rnorms, const uint8_t* v_codes, const uint16_t* v_norms,
+                                   int key_bits, int value_bits, int has_qjl, const float* key_rotation,
+                                   const float* key_centers, const float* qjl, const float* value_rotation,
+                                   const float* value_centers, float scale, float* out_f32, uint16_t* out_bf16,
+                                   float* lse_out, void* workspace, size_t workspace_bytes, void* stream) {
+    return decode_attention_impl(q, batch, q_heads, kv_heads, dim, seq_starts, seq_lens, n_tokens, cap, k_codes,
+                                 k_norms, k_signs, k_rnorms, v_codes, v_norms, key_bits, value_bits, has_qjl,
+                                 key_rotation, key_centers, qjl, value_rotation, value_centers, scale, out_f32,
+                                 out_bf16, lse_out, workspace, workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------ no-allocation entry point
+// The partials of tq_decode_attention_noalloc: one copy per GPU, held until the process ends.
+// In host code `scratch` names a host-side stand-in, not device memory: the device address
+// of each GPU's copy comes from hipGetSymbolAddress, made once per device (with that device
+// current) on the first call there, and only that address is ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[TQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[MAX_DEVICES];  // device address of `scratch` on each device, once resolved
+
+int device_scratch(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return TQ_ERR_HIP;
+    if (dev < 0 || dev >= MAX_DEVICES) return TQ_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return TQ_ERR_HIP;
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return TQ_OK;
+}
+}  // namespace
+
+extern "C" int tq_decode_attention_noalloc(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
+                                           const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens,
+                                           int64_t cap, const uint8_t* k_codes, const uint16_t* k_norms,
+                                           const uint8_t* k_signs, const uint16_t* k_rnorms, const uint8_t* v_codes,
+                                           const uint16_t* v_norms, int key_bits, int value_bits, int has_qjl,
+                                           const float* key_rotation, const float* key_centers, const float* qjl,
+                                           const float* value_rotation, const float* value_centers, float scale,
+                                           float* out_f32, uint16_t* out_bf16, float* lse_out, void* stream) {
+    void* ws = nullptr;
+    const int st = device_scratch(&ws);
+    if (st != TQ_OK) return st;
+    // the shared body sizes the partials for this call and returns TQ_ERR_WORKSPACE, before
+    // any launch, when they exceed the array
+    return decode_attention_impl(q, batch, q_heads, kv_heads, dim, seq_starts, seq_lens, n_tokens, cap, k_codes,
+                                 k_norms, k_signs, k_rnorms, v_codes, v_norms, key_bits, value_bits, has_qjl,
+                                 key_rotation, key_centers, qjl, value_rotation, value_centers, scale, out_f32,
+                                 out_bf16, lse_out, ws, TQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int tq_decode_attention_groups(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,

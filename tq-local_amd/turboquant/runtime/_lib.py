@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple] = {
     "tq_decode_attention_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I64]),
     "tq_decode_attention": (_I, [_P, _I, _I, _I, _I, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                                  _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _SZ, _P]),
+    "tq_decode_attention_noalloc": (_I, [_P, _I, _I, _I, _I, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I, _I,
+                                         _I, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P]),
     "tq_dequantize_mse": (_I, [_P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "tq_dequantize_prod": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P]),
     "tq_group_matrix": (_I, [_P, _I, _P, _I, _P]),
