@@ -134,3 +134,45 @@ def test_valid_range_from_masks():
     s2, e2 = _valid_range(add, 3, 4, "cpu")
     assert s2.tolist() == s.tolist() and e2.tolist() == e.tolist()
     assert _valid_range(None, 3, 4, "cpu") == (None, None)
+
+
+def test_valid_range_rejects_masks_with_holes():
+    """Right padding followed by generated tokens leaves a hole; the fused kernel takes one
+    range per row, so the range helper refuses such a mask (fused_attention then returns
+    None) unless the caller vouches for contiguity."""
+    from turboquant.runtime.attention import _HoleyMask
+
+    m = torch.tensor([[1, 1, 1, 1, 1], [1, 1, 0, 0, 1]], dtype=torch.bool)
+    with pytest.raises(_HoleyMask):
+        _valid_range(m[:, None, None, :], 2, 5, "cpu")
+    s, e = _valid_range(m[:, None, None, :], 2, 5, "cpu", check_contiguous=False)
+    assert s.tolist() == [0, 0] and e.tolist() == [5, 5]
+    left = torch.tensor([[0, 0, 1, 1, 1]], dtype=torch.bool)  # left padding stays contiguous
+    s, e = _valid_range(left, 1, 5, "cpu")
+    assert s.tolist() == [2] and e.tolist() == [5]
+
+
+def test_loader_takes_local_directories_only(tmp_path):
+    """No hub downloads in this build: a model id that is not a local directory raises
+    FileNotFoundError before transformers is asked to fetch anything."""
+    from turboquant.adapters.transformers import TransformersLoadConfig, TurboQuantSession, load_transformers_model
+
+    with pytest.raises(FileNotFoundError, match="local model directory"):
+        load_transformers_model(TransformersLoadConfig("some-org/some-model"))
+    with pytest.raises(FileNotFoundError):
+        TurboQuantSession.from_pretrained(str(tmp_path / "missing"))
+
+
+def test_session_settings_and_bit_checks():
+    from turboquant.adapters.transformers import TurboQuantSession
+
+    model = tiny_llama()
+    s = TurboQuantSession(model=model, tokenizer=CharTokenizer())
+    # the reference's session defaults differ from activate's
+    assert (s.bits, s.use_qjl_keys, s.quantize_decode, s.variant) == (3, False, False, "qmse_packed")
+    assert s.compatibility_report()["compatible"] and s.last_telemetry() is None
+    with pytest.raises(ValueError, match="unsupported"):
+        TurboQuantSession(model=model, tokenizer=CharTokenizer(), bits=1, use_qjl_keys=True)
+    with pytest.raises(ValueError, match="out of range"):
+        turboquant.activate(model, CharTokenizer(), bits=4, num_outlier_channels=4, outlier_extra_bits=5, quiet=True)
+    assert not turboquant.is_active(model)

@@ -540,7 +540,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     const int64_t t0 = r0;
     const int64_t t1 = r1 > r0 ? r1 : r0;
     const int64_t ntok = t1 - t0;
-    // token offsets within the range are 32-bit: the host keeps the range below 2^25 tokens
+    // token offsets within the range are 32-bit: the host keeps the range below 2^24 tokens
     const int nt = (int)ntok;
     constexpr int STEP = NW * BLK;
     const size_t row0 = (size_t)grp * cap + (size_t)(t0 < n_tokens ? t0 : 0);
@@ -566,13 +566,18 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     const int vo = 4 * vdw + g * VROW;           // + 4 r VROW for token 4 r + g (each load: 4 whole rows)
     const int vsh = vbit0 - 32 * vdw;            // in [0, 64) for VB == 3, [0, 32) otherwise
 
-    struct Blk {
+    // Per-block data of a wave, in the part the score stage reads (key codes, sign bits and
+    // the three norms of token n) and the part the value stage reads (value codes of tokens
+    // 4 r + g).
+    struct Kd {
         uint32_t kw[KB];      // key codes of token n, dims [32 g, 32 g + 32)
         uint32_t sw;          // sign bits of token n, same dims
         uint32_t kn, kr, vn;  // norms (f16 bits) of token n
+    };
+    struct Vd {
         uint32_t vw[4][2];    // value codes of tokens 4 r + g, lane n's dword(s)
     };
-    auto load = [&](Blk& B, int rel_) {
+    auto load_k = [&](Kd& B, int rel_) {
         const int rel = __builtin_amdgcn_readfirstlane(rel_);  // scalar block offset
         if constexpr (KB == 1) {
             B.kw[0] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko, rel * KROW, KV_NT);
@@ -595,6 +600,9 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         }
         B.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn, no, rel * 2, KV_NT);
         B.vn = __builtin_amdgcn_raw_buffer_load_b16(rvn, no, rel * 2, KV_NT);
+    };
+    auto load_v = [&](Vd& B, int rel_) {
+        const int rel = __builtin_amdgcn_readfirstlane(rel_);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             if constexpr (VB == 3) {
@@ -678,7 +686,17 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     constexpr int KSHIFT = Sm::KC == 32 ? 8 : (Sm::KC == 8 ? 6 : 3);  // log2 bytes per key-table entry row
     const uint32_t klane = 8u * (uint32_t)(lane & (Sm::KC - 1));
 
-    auto process = [&](const Blk& B, int rel) {
+    // The value MFMAs' A operand for one block: the softmax weights, transposed through LDS
+    // (paired layout: one u32x4 per MFMA half)
+    constexpr int NAV = PV ? 2 : 1;
+    struct Av {
+        u32x4 a[NAV];
+    };
+
+    // ---- score stage, part 1: key-score and QJL MFMAs, then the scores (log2 domain) of
+    // token n for this lane's heads, -inf for tokens past the range.  Returns whether any
+    // score exceeds its head's lazy threshold (wave-uniform).
+    auto scores = [&](const Kd& B, int rel, float (&lg)[R::HPL]) -> bool {
         // ---- key scores: 8 MFMAs over dims 32 g + 4 j + r
         // two independent accumulation chains (even / odd j) halve the dependent MFMA latency
         f32x4 acc_k = f32x4{0.f, 0.f, 0.f, 0.f}, acc_k1 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -717,15 +735,12 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             }
         }
         __builtin_amdgcn_s_setprio(0);
-        // ---- scores (log2 domain) of token n for this lane's heads
         // valid tokens of the block: a scalar count, one compare per lane
         const int nvalid = __builtin_amdgcn_readfirstlane(nt - rel < BLK ? nt - rel : BLK);
         const bool valid = n < nvalid;
         // the f16 norms enter v_fma_mix_f32 as they are (no separate conversions)
         const float knf = tq::f16_to_f32(B.kn);
         const float krf = QJL ? tq::f16_to_f32(B.kr) : 0.0f;
-        const float vnf = tq::f16_to_f32(B.vn);  // invalid tokens get p = 0 below
-        float lg[R::HPL];
         bool over = false;
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i) {
@@ -749,27 +764,38 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             lg[i] = valid ? v : NEG_INF;
             over |= lg[i] > m_thr[i];
         }
-        // ---- online softmax with a lazily raised reference maximum
-        if (__builtin_amdgcn_ballot_w64(over)) {
+        return __builtin_amdgcn_ballot_w64(over) != 0;
+    };
+
+    // ---- the lazy reference maximum raised (rare): partial sums and value accumulators
+    // rescaled to the new maximum
+    auto raise_max = [&](const float (&lg)[R::HPL]) {
 #pragma unroll
-            for (int i = 0; i < R::HPL; ++i) {
-                const float mn = fmaxf(m_ref[i], row_max16(lg[i]));
-                const float a = m_ref[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_ref[i] - mn);  // 1 if unchanged
-                s_lane[i] *= a;
-                if constexpr (PV) {
+        for (int i = 0; i < R::HPL; ++i) {
+            const float mn = fmaxf(m_ref[i], row_max16(lg[i]));
+            const float a = m_ref[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_ref[i] - mn);  // 1 if unchanged
+            s_lane[i] *= a;
+            if constexpr (PV) {
 #pragma unroll
-                    for (int m = 0; m < NACC; ++m) acc_v[m] *= a;  // all four rows are this lane's head
-                } else {
+                for (int m = 0; m < NACC; ++m) acc_v[m] *= a;  // all four rows are this lane's head
+            } else {
 #pragma unroll
-                    for (int m = 0; m < NACC; ++m) {
-                        acc_v[m][2 * i] *= a;
-                        acc_v[m][2 * i + 1] *= a;
-                    }
+                for (int m = 0; m < NACC; ++m) {
+                    acc_v[m][2 * i] *= a;
+                    acc_v[m][2 * i + 1] *= a;
                 }
-                m_ref[i] = mn;
-                m_thr[i] = mn + LAZY_MAX;
             }
+            m_ref[i] = mn;
+            m_thr[i] = mn + LAZY_MAX;
         }
+    };
+
+    // ---- score stage, part 2: the softmax weights p |v| of token n (hi and lo bf16 parts)
+    // into the value MFMAs' A operand, transposed through this wave's LDS rows (one wave's
+    // LDS accesses execute in order and the compiler keeps the may-alias writes and reads of
+    // wt in program order, so no fence is needed)
+    auto weights = [&](const float (&lg)[R::HPL], uint32_t vn_bits, Av& av) {
+        const float vnf = tq::f16_to_f32(vn_bits);  // invalid tokens have p = 0
         uint32_t wq[R::HPL][2];
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i) {
@@ -781,15 +807,14 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             wq[i][0] = hh;
             wq[i][1] = dup_bf16(w - __uint_as_float(hh & 0xFFFF0000u));
         }
-        // ---- weights -> A operand of the value MFMAs (transpose through this wave's LDS rows;
-        // one wave's LDS accesses execute in order and the compiler keeps the may-alias
-        // writes and reads of wt in program order, so no fence is needed)
         if constexpr (PV) {
             // rows 4 h + 2 p + x: this lane's head is g; the zero slots are never written
             wt[4 * g + 0][pslot] = wq[0][0];
             wt[4 * g + 1][pslot] = wq[0][1];
             wt[4 * g + 2][pslot + 1] = wq[0][0];
             wt[4 * g + 3][pslot + 1] = wq[0][1];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) av.a[u] = *reinterpret_cast<const u32x4*>(&wt[n][4 * (4 * u + g)]);
         } else {
 #pragma unroll
             for (int i = 0; i < R::HPL; ++i) {
@@ -797,14 +822,18 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                 wt[R::row(h, 0)][wslot] = wq[i][0];
                 wt[R::row(h, 1)][wslot] = wq[i][1];
             }
+            av.a[0] = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
         }
+    };
+
+    // ---- value stage: the value MFMAs of one block
+    auto values = [&](const Vd& B, const Av& av) {
         __builtin_amdgcn_s_setprio(1);
         if constexpr (PV) {
-            // ---- value MFMAs, paired: lane (c = n, k = g) supplies tokens 8 u + 4 s + g, pair
-            // column c of group m = code byte m of dword c (dims 8 c + 2 m, 8 c + 2 m + 1)
+            // paired: lane (c = n, k = g) supplies tokens 8 u + 4 s + g, pair column c of group
+            // m = code byte m of dword c (dims 8 c + 2 m, 8 c + 2 m + 1)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * (4 * u + g)]);
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     // LDS byte offset 256 * byte m + plane in one v_perm: [plane, byte m, 0, 0]
@@ -814,12 +843,11 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                     const uint32_t o1 = __builtin_amdgcn_perm(B.vw[2 * u + 1][0], plane, sel);
                     const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
                     const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
-                    acc_v[m] = mfma_bf16(av, u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
+                    acc_v[m] = mfma_bf16(av.a[u], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
                 }
             }
         } else {
-            const u32x4 av = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
-            // ---- value MFMAs: lane (n, g) supplies tokens 4 r + g (k-slots 8 g + 2 r + y), dim 8 n + m
+            // lane (n, g) supplies tokens 4 r + g (k-slots 8 g + 2 r + y), dim 8 n + m
             uint32_t vch[4][2];  // VB = 4: [r][0] = chunk << 2 (even codes), [r][1] = chunk >> 2 (odd codes)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -848,7 +876,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                     }
                     bv[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.vtab) + off);
                 }
-                acc_v[m] = mfma_bf16(av, bv, acc_v[m]);
+                acc_v[m] = mfma_bf16(av.a[0], bv, acc_v[m]);
             };
             vmfma(std::integral_constant<int, 0>{});
             vmfma(std::integral_constant<int, 1>{});
@@ -867,20 +895,29 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     const int nb = first < nt ? (nt - first + STEP - 1) / STEP : 0;
     if (nb > 0) {
         // two of this wave's blocks in flight: while one is processed the next-but-one is
-        // loaded into the register set just consumed, so A and Bq alternate without copies
-        Blk A, Bq;
+        // loaded into the register set just consumed, so A and B alternate without copies
+        Kd ka, kb;
+        Vd va, vb;
+        auto process = [&](const Kd& K_, const Vd& V_, int rel) {
+            float lg[R::HPL];
+            if (scores(K_, rel, lg)) raise_max(lg);
+            Av av;
+            weights(lg, K_.vn, av);
+            values(V_, av);
+        };
         int rel = first;
-        load(A, rel);
-        if (nb > 1) load(Bq, rel + STEP);
+        load_k(ka, rel);
+        load_v(va, rel);
+        if (nb > 1) load_k(kb, rel + STEP), load_v(vb, rel + STEP);
         int i = 0;
         for (; i + 2 <= nb; i += 2) {
-            process(A, rel);
-            if (i + 2 < nb) load(A, rel + 2 * STEP);
-            process(Bq, rel + STEP);
-            if (i + 3 < nb) load(Bq, rel + 3 * STEP);
+            process(ka, va, rel);
+            if (i + 2 < nb) load_k(ka, rel + 2 * STEP), load_v(va, rel + 2 * STEP);
+            process(kb, vb, rel + STEP);
+            if (i + 3 < nb) load_k(kb, rel + 3 * STEP), load_v(vb, rel + 3 * STEP);
             rel += 2 * STEP;
         }
-        if (i < nb) process(A, rel);
+        if (i < nb) process(ka, va, rel);
     }
 
     // ------------------------------------------------------------ epilogue
@@ -1001,9 +1038,9 @@ int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out
     const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC, QJL>::NW, &tps);
     *n_split_out = ns;
     *tps_out = tps;
-    // a workgroup's range stays below 2^25 tokens: its byte ranges fit the 31-bit buffer
+    // a workgroup's range stays below 2^24 tokens: its byte ranges fit the 31-bit buffer
     // descriptors and its token offsets fit 32-bit scalars
-    if (tps >= ((int64_t)1 << 25)) return TQ_ERR_UNSUPPORTED;
+    if (tps >= ((int64_t)1 << 24)) return TQ_ERR_UNSUPPORTED;
     if (a.po == nullptr) return TQ_OK;  // sizing query only
     hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC, QJL>::NT), 0, s, a.q, a.q_heads,
                        a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
