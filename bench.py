@@ -319,6 +319,55 @@ def bench_c5(args, dev) -> dict:
     }
 
 
+def bench_host(args, dev) -> dict:
+    """Host cost of one decode-attention call: the Python path an HF decode step takes
+    (fused_attention on a packed cache layer) and the bare libtq wrapper, timed over many
+    back-to-back calls on a small layer (the device time per call is reported beside it,
+    so a host-bound loop shows as wall time above device time)."""
+    import torch
+
+    from turboquant.runtime import kernels as K
+    from turboquant.runtime.attention import fused_attention
+    from turboquant.runtime.packed_qmse_cache import PackedMSELayer
+    from turboquant.runtime.synthetic import kv_bf16, query_bf16
+
+    B, Hq, Hkv, N, D = 1, 40, 8, 4096, 128  # config-5 heads, a short history
+    layer = PackedMSELayer(bits=4, use_qjl_keys=True, quantize_decode=True)
+    layer.initialize_from_dense(kv_bf16((B, Hkv, N, D), seed=1, device=dev), kv_bf16((B, Hkv, N, D), seed=2, device=dev))
+    q = query_bf16(B, Hq, D, seed=3, device=dev).unsqueeze(2)
+    mask = torch.ones(B, 1, 1, N, dtype=torch.bool, device=dev)
+    s, c = layer._store, layer.codecs
+    calls = {
+        "fused_attention": lambda: fused_attention(q, layer, Hq // Hkv),
+        "fused_attention_masked": lambda: fused_attention(q, layer, Hq // Hkv, mask),
+        "kernels.decode_attention": lambda: K.decode_attention(
+            q, k_codes=s.kc, k_norms=s.kn, v_codes=s.vc, v_norms=s.vn, n_tokens=N, key=c.key, value=c.value,
+            k_signs=s.ks, k_rnorms=s.kr, qjl=c.qjl),
+    }
+    out = {}
+    for name, fn in calls.items():
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        reps = 2000
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        t_host = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter() - t0
+        out[name] = {"host_us_per_call": round(t_host / reps * 1e6, 2),
+                     "wall_us_per_call": round(t_wall / reps * 1e6, 2),
+                     "device_us_per_call": round(e0.elapsed_time(e1) * 1e3 / reps, 2)}
+        print(f"[bench] host {name}: {out[name]}", file=sys.stderr, flush=True)
+    return {"metric": "decode-attention host cost per call", "unit": "us",
+            "config": {"workload": f"B={B}, Hq={Hq}, Hkv={Hkv}, N={N}, 4-bit Q_prod, 2000 back-to-back calls"},
+            "calls": out}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -343,6 +392,8 @@ def main() -> int:
     ap.add_argument("--c5-layers", type=int, default=64)
     ap.add_argument("--c5-prompt", type=int, default=131072)
     ap.add_argument("--c5-new", type=int, default=512)
+    ap.add_argument("--host", action="store_true",
+                    help="host cost per decode-attention call (Python wrappers) instead of the C2 line")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -366,6 +417,9 @@ def main() -> int:
         return 0
     if args.c5:
         print(json.dumps(bench_c5(args, dev)))
+        return 0
+    if args.host:
+        print(json.dumps(bench_host(args, dev)))
         return 0
     B, Hq, Hkv, N, D, bits = args.batch, args.q_heads, args.kv_heads, args.context, 128, args.bits
     qjl = not args.no_qjl

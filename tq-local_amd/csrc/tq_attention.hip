@@ -216,13 +216,14 @@ struct Rows {
 };
 
 // Value MFMA layouts.  Generic: rows (head, w hi|lo), columns = 16 dims, k-slots = 16 tokens
-// x (Cv hi, Cv lo), one 4-byte table lookup per code.  Paired (4-bit values, at most 4
+// x (Cv hi, Cv lo), one 4-byte table lookup per code.  Paired (3- and 4-bit values, at most 4
 // heads): rows (head, dim parity p, w hi|lo) fill all 16 rows, columns = 16 pairs of
-// adjacent dims, k-slots = 8 tokens x parity x (Cv hi, Cv lo); one 8-byte lookup per code
-// byte returns both dims of a pair, and the A operand is zero where the parities differ.
+// adjacent dims, k-slots = 8 tokens x parity x (Cv hi, Cv lo); one 8-byte lookup per pair
+// of codes (a code byte at 4 bits, a 6-bit field at 3 bits) returns both dims of a pair,
+// and the A operand is zero where the parities differ.
 template <int VB, int GC>
-constexpr bool PAIRED = GC == 1 && VB == 4;
-constexpr int VCOPIES = 32;      // lane-private copies of the 256-entry pair table (bank pair per lane)
+constexpr bool PAIRED = GC == 1 && (VB == 4 || VB == 3);
+constexpr int VCOPIES = 32;      // lane-private copies of the pair table (bank pair per lane)
 constexpr int WT_STRIDE_P = 36;  // dwords per weight row in the paired layout (32 slots + bank spread)
 
 // LDS scratch of the image builder
@@ -248,9 +249,9 @@ struct Smem {
     // copy c at byte 8 (KC e + c), so the lanes of a 32-lane LDS pass use distinct bank pairs
     static constexpr int KC = KCOPIES<KB, PV>;
     uint2 ktab[1 << (2 * KB)][KC];
-    // paired: (Cv hi|lo of the low nibble, Cv hi|lo of the high nibble) per code byte, entry e
-    // of copy c at byte 256 e + 8 c from the table base
-    uint2 vtab2[PV ? 256 : 1][PV ? VCOPIES : 1];
+    // paired: (Cv hi|lo of the even dim's code, Cv hi|lo of the odd dim's code) per pair of
+    // codes (2^(2 VB) entries), entry e of copy c at byte 256 e + 8 c from the table base
+    uint2 vtab2[PV ? (1 << (2 * VB)) : 1][PV ? VCOPIES : 1];
     uint32_t vtab[1 << VB];             // Cv hi|lo per value code (generic layout)
     uint32_t wt[NW][16][WTS];           // per-wave transpose of the softmax weights
     union {
@@ -633,9 +634,9 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         (&sm.ktab[0][0])[i] = make_uint2(sm.u.pro.ksrc[e & ((1 << KB) - 1)], sm.u.pro.ksrc[e >> KB]);
     }
     if constexpr (Sm::PV) {
-        for (int i = tid; i < 256 * VCOPIES; i += NT) {
+        for (int i = tid; i < (1 << (2 * VB)) * VCOPIES; i += NT) {
             const int e = i / VCOPIES;
-            (&sm.vtab2[0][0])[i] = make_uint2(sm.vtab[e & 15], sm.vtab[e >> 4]);
+            (&sm.vtab2[0][0])[i] = make_uint2(sm.vtab[e & ((1 << VB) - 1)], sm.vtab[e >> VB]);
         }
     }
     const uint32_t* im = reinterpret_cast<const uint32_t*>(sm.u.pro.img);
@@ -829,9 +830,28 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // ---- value stage: the value MFMAs of one block
     auto values = [&](const Vd& B, const Av& av) {
         __builtin_amdgcn_s_setprio(1);
-        if constexpr (PV) {
-            // paired: lane (c = n, k = g) supplies tokens 8 u + 4 s + g, pair column c of group
-            // m = code byte m of dword c (dims 8 c + 2 m, 8 c + 2 m + 1)
+        if constexpr (PV && VB == 3) {
+            // paired, 3-bit: lane (c = n, k = g) supplies tokens 8 u + 4 s + g; the 24-bit chunk of
+            // dims 8 c .. 8 c + 7 is aligned to bit 0, and pair m (dims 8 c + 2 m, 8 c + 2 m + 1)
+            // is its 6-bit field m: LDS byte offset 256 * field + plane in two VALU ops
+            uint32_t ch[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                ch[r] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh) : B.vw[r][1] >> (vsh - 32);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const uint32_t o0 = field_x<6, 8>(&ch[2 * u], 6 * m) | plane;
+                    const uint32_t o1 = field_x<6, 8>(&ch[2 * u + 1], 6 * m) | plane;
+                    const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
+                    const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
+                    acc_v[m] = mfma_bf16(av.a[u], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
+                }
+            }
+        } else if constexpr (PV) {
+            // paired, 4-bit: lane (c = n, k = g) supplies tokens 8 u + 4 s + g, pair column c of
+            // group m = code byte m of dword c (dims 8 c + 2 m, 8 c + 2 m + 1)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
 #pragma unroll

@@ -52,6 +52,12 @@ def _attend_mask(attention_mask: torch.Tensor, B: int, total: int) -> torch.Tens
     return m
 
 
+#: the ranges of the last mask seen (an HF forward hands every layer the same mask tensor):
+#: (mask, its version counter, B, total, check) -> (starts, ends); holding the mask keeps its
+#: memory from being reused by another tensor while the entry is live
+_last_range: tuple | None = None
+
+
 def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device, check_contiguous: bool = True):
     """Per-row attended slot range [start, end) from an HF decode mask.
 
@@ -59,10 +65,28 @@ def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device
     kernel attends to every slot of the range, so a row whose attended slots have a
     hole (right padding followed by generated tokens) cannot take this path: with
     ``check_contiguous`` such masks raise ``_HoleyMask`` (one host sync to find out);
-    callers that know the mask's shape pass False.
+    callers that know the mask's shape pass False.  The result for one mask tensor is
+    computed once and reused by the following layers of the same forward.
     """
+    global _last_range
     if attention_mask is None:
         return None, None
+    c = _last_range
+    if (c is not None and c[0] is attention_mask and c[1] == attention_mask._version
+            and c[2:6] == (B, total, check_contiguous, device)):
+        if c[6] is None:
+            raise _HoleyMask
+        return c[6]
+    try:
+        result = _compute_range(attention_mask, B, total, device, check_contiguous)
+    except _HoleyMask:
+        _last_range = (attention_mask, attention_mask._version, B, total, check_contiguous, device, None)
+        raise
+    _last_range = (attention_mask, attention_mask._version, B, total, check_contiguous, device, result)
+    return result
+
+
+def _compute_range(attention_mask: torch.Tensor, B: int, total: int, device, check_contiguous: bool):
     m = _attend_mask(attention_mask, B, total)
     idx = torch.arange(m.shape[1], device=m.device, dtype=torch.int32)
     big = torch.iinfo(torch.int32).max
@@ -125,7 +149,8 @@ def fused_attention(query_states: torch.Tensor, packed_layer: "PackedMSELayer", 
                                     check_contiguous=known is None)
     except _HoleyMask:
         return None
-    p_ends = None if ends is None else torch.clamp(ends, max=n_packed)
+    # the kernel sees the packed slots only; ends beyond them (dense tokens) are clamped
+    p_ends = ends if ends is None or n_dense == 0 else torch.clamp(ends, max=n_packed)
     f32 = query_states.dtype == torch.float32
     kw = dict(n_tokens=n_packed, seq_starts=starts, seq_lens=p_ends, scale=scale, want_f32=f32 or n_dense > 0,
               want_lse=n_dense > 0)

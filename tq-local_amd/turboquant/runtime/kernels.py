@@ -227,6 +227,8 @@ def dequantize_prod(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Tenso
 
 #: partials workspace per (device, stream): calls on one stream are ordered, so they can
 #: share one; calls on two streams get two
+#: partials workspace per (device, stream): calls on one stream are ordered, so they can
+#: share one; calls on two streams get two
 _workspaces: dict[tuple, torch.Tensor] = {}
 #: workspaces replaced by a larger one stay allocated: a HIP graph that captured a call keeps
 #: the old pointer and may be replayed later
@@ -234,8 +236,7 @@ _retired: list[torch.Tensor] = []
 _ws_bytes: dict[tuple, int] = {}
 
 
-def attention_workspace(device: torch.device, batch: int, q_heads: int, kv_heads: int, max_tokens: int) -> torch.Tensor:
-    """The partials workspace of ``tq_decode_attention`` for the current stream of ``device``."""
+def _workspace_for(device: torch.device, stream: int, batch: int, q_heads: int, kv_heads: int) -> torch.Tensor:
     shape = (batch, q_heads, kv_heads)
     need = _ws_bytes.get(shape)
     if need is None:
@@ -244,7 +245,7 @@ def attention_workspace(device: torch.device, batch: int, q_heads: int, kv_heads
         if need == 0:
             raise ValueError("invalid attention shape for workspace sizing")
         _ws_bytes[shape] = need
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = (device.index, stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:
         if ws is not None:
@@ -252,6 +253,15 @@ def attention_workspace(device: torch.device, batch: int, q_heads: int, kv_heads
         ws = torch.empty(need, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
+
+
+def attention_workspace(device: torch.device, batch: int, q_heads: int, kv_heads: int, max_tokens: int) -> torch.Tensor:
+    """The partials workspace of ``tq_decode_attention`` for the current stream of ``device``."""
+    return _workspace_for(device, torch.cuda.current_stream(device).cuda_stream, batch, q_heads, kv_heads)
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
 
 
 def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.Tensor, v_codes: torch.Tensor,
@@ -267,32 +277,47 @@ def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.T
     attends to slots [seq_starts[b], seq_lens[b]) when those are given.
     Returns bf16 [B, Hq, D], then fp32 [B, Hq, D] if ``want_f32`` and the fp32
     log-sum-exp [B, Hq] of the scaled logits if ``want_lse``.
+
+    This runs once per layer and decode step, so the host path is kept short: one
+    stream lookup, plain integer pointers into the ctypes call, no copies of inputs
+    that are already bf16 and contiguous.
     """
     if q.dim() == 4:
         if q.shape[2] != 1:
             raise ValueError("decode_attention takes exactly one query token per sequence")
         q = q[:, :, 0, :]
-    q = q.to(torch.bfloat16).contiguous()
-    _require_gpu(q, k_codes, v_codes)
+    if q.dtype != torch.bfloat16:
+        q = q.to(torch.bfloat16)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    if not (q.is_cuda and k_codes.is_cuda and v_codes.is_cuda):
+        _require_gpu(q, k_codes, v_codes)
     B, Hq, D = q.shape
     Hkv, cap = k_codes.shape[1], k_codes.shape[2]
-    has_qjl = k_signs is not None
-    out_bf16 = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=q.device)
-    out_f32 = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device) if want_f32 else None
-    ws = attention_workspace(q.device, B, Hq, Hkv, max(int(n_tokens), 1))
-    lse = torch.empty(B, Hq, dtype=torch.float32, device=q.device) if want_lse else None
-    if seq_lens is not None:
-        seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
-    if seq_starts is not None:
-        seq_starts = seq_starts.to(device=q.device, dtype=torch.int32).contiguous()
+    dev = q.device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out_bf16 = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
+    out_f32 = torch.empty((B, Hq, D), dtype=torch.float32, device=dev) if want_f32 else None
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if want_lse else None
+    ws = _workspace_for(dev, stream, B, Hq, Hkv)
+    if seq_lens is not None and (seq_lens.dtype != torch.int32 or seq_lens.device != dev
+                                 or not seq_lens.is_contiguous()):
+        seq_lens = seq_lens.to(device=dev, dtype=torch.int32).contiguous()
+    if seq_starts is not None and (seq_starts.dtype != torch.int32 or seq_starts.device != dev
+                                   or not seq_starts.is_contiguous()):
+        seq_starts = seq_starts.to(device=dev, dtype=torch.int32).contiguous()
     s = float(scale) if scale is not None else 1.0 / math.sqrt(D)
-    _lib.call("tq_decode_attention", _vp(q), B, Hq, Hkv, D, _vp(seq_starts), _vp(seq_lens), int(n_tokens), cap,
-              _vp(k_codes), _vp(k_norms), _vp(k_signs), _vp(k_rnorms), _vp(v_codes), _vp(v_norms),
-              key.bits, value.bits, int(has_qjl), _vp(key.rotation), _vp(key.centers), _vp(qjl),
-              _vp(value.rotation), _vp(value.centers), ctypes.c_float(s), _vp(out_f32), _vp(out_bf16),
-              _vp(lse), _vp(ws), ws.numel(), _stream(q.device))
-    outs = (out_bf16,) + ((out_f32,) if want_f32 else ()) + ((lse,) if want_lse else ())
-    return outs if len(outs) > 1 else out_bf16
+    fn = _lib.load().tq_decode_attention
+    st = fn(q.data_ptr(), B, Hq, Hkv, D, _ptr(seq_starts), _ptr(seq_lens), int(n_tokens), cap,
+            k_codes.data_ptr(), k_norms.data_ptr(), _ptr(k_signs), _ptr(k_rnorms), v_codes.data_ptr(),
+            v_norms.data_ptr(), key.bits, value.bits, int(k_signs is not None), key.rotation.data_ptr(),
+            key.centers.data_ptr(), _ptr(qjl), value.rotation.data_ptr(), value.centers.data_ptr(), s,
+            _ptr(out_f32), out_bf16.data_ptr(), _ptr(lse), ws.data_ptr(), ws.numel(), stream)
+    if st != _lib.TQ_OK:
+        _lib.check("tq_decode_attention", st)
+    if want_f32:
+        return (out_bf16, out_f32, lse) if want_lse else (out_bf16, out_f32)
+    return (out_bf16, lse) if want_lse else out_bf16
 
 
 def decode_attention_groups(q: torch.Tensor, groups: list[dict], *, n_tokens: int, key_stack: torch.Tensor,
