@@ -77,6 +77,61 @@ def test_quantize_prod_bit_exact(cuda, bits):
     assert np.array_equal(u16(rnorms).reshape(-1), rr)
 
 
+def _matrix_core_input(cuda, seed, T=2101):
+    """[2, 3, T, D] bf16 keys as a strided [B, H, T, D] view of a [B, T, H, D] buffer, with the
+    special rows at tokens 100..105: 6 T vectors (>= 4096, so the matrix-core encoder runs),
+    a tile count that is not a multiple of 16 vectors."""
+    x = kv_bf16((2, 3, T, D), seed=seed, device=cuda)
+    x[:, :, 100:106] = _special_rows(cuda)[0, 0]
+    x = x.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    assert not x.is_contiguous() and x.shape[0] * x.shape[1] * x.shape[2] % 16 != 0
+    return x
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_quantize_mse_matrix_core_bit_exact(cuda, bits):
+    x = _matrix_core_input(cuda, 30 + bits)
+    codec = layer_codecs(D, bits, 0, False, cuda).value
+    B, H, n, _ = x.shape
+    cap, off = n + 7, 3
+    codes = torch.zeros(B, H, cap, K.row_bytes(D, bits), dtype=torch.uint8, device=cuda)
+    norms = torch.zeros(B, H, cap, dtype=torch.float16, device=cuda)
+    K.quantize_mse(x, codec, codes, norms, offset=off)
+    torch.cuda.synchronize()
+    R, _, bnd = _host(codec)
+    rc, rn = O.encode_mse(u16(x).reshape(-1, D), bits, R, bnd)
+    got_c = codes[:, :, off:off + n].cpu().numpy().reshape(-1, rc.shape[1])
+    assert np.array_equal(got_c, rc), f"{(got_c != rc).sum()} code bytes differ"
+    assert np.array_equal(u16(norms[:, :, off:off + n]).reshape(-1), rn)
+    assert int(codes[:, :, :off].count_nonzero()) == 0 and int(codes[:, :, off + n:].count_nonzero()) == 0
+    assert int(norms[:, :, :off].count_nonzero()) == 0 and int(norms[:, :, off + n:].count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_quantize_prod_matrix_core_bit_exact(cuda, bits):
+    x = _matrix_core_input(cuda, 50 + bits)
+    lc = layer_codecs(D, bits, 0, True, cuda)
+    B, H, n, _ = x.shape
+    cap, off = n + 5, 2
+    codes = torch.zeros(B, H, cap, K.row_bytes(D, bits - 1), dtype=torch.uint8, device=cuda)
+    norms = torch.zeros(B, H, cap, dtype=torch.float16, device=cuda)
+    signs = torch.zeros(B, H, cap, D // 8, dtype=torch.uint8, device=cuda)
+    rnorms = torch.zeros(B, H, cap, dtype=torch.float16, device=cuda)
+    K.quantize_prod(x, lc.key, lc.qjl, codes, norms, signs, rnorms, offset=off)
+    torch.cuda.synchronize()
+    R, C, bnd = _host(lc.key)
+    rc, rn, rs, rr = O.encode_prod(u16(x).reshape(-1, D), bits - 1, R, C, bnd, lc.qjl.cpu().numpy())
+    sl = slice(off, off + n)
+    got_c = codes[:, :, sl].cpu().numpy().reshape(rc.shape)
+    got_s = signs[:, :, sl].cpu().numpy().reshape(rs.shape)
+    assert np.array_equal(got_c, rc), f"{(got_c != rc).sum()} code bytes differ"
+    assert np.array_equal(u16(norms[:, :, sl]).reshape(-1), rn)
+    assert np.array_equal(got_s, rs), f"{(got_s != rs).sum()} sign bytes differ"
+    assert np.array_equal(u16(rnorms[:, :, sl]).reshape(-1), rr)
+    for t in (codes, norms, signs, rnorms):
+        assert int(t[:, :, :off].count_nonzero()) == 0 and int(t[:, :, off + n:].count_nonzero()) == 0
+
+
 def test_quantize_strided_input_and_decode_append(cuda):
     """A [B,T,H,D] buffer viewed as [B,H,T,D] (HF layout), appended one token at a time."""
     base = kv_bf16((1, 4, 40, D), seed=7, device=cuda)  # [B, T=4?]

@@ -18,6 +18,8 @@
 // (_encode_keys_qjl_group), :404-435 (_decode_group), :13-43 (_pack_indices),
 // :148-154 (_pack_qjl_signs).
 
+#include <algorithm>
+
 #include "tq_common.h"
 
 namespace {
@@ -135,7 +137,7 @@ __device__ __forceinline__ uint32_t bucket_search(float z, const float* __restri
 #pragma unroll
     for (int lvl = 0; lvl < BITS; ++lvl) {
         const int s = 1 << (BITS - 1 - lvl);
-        float cand[1 << lvl];
+        float cand[1 << (BITS - 1)];
 #pragma unroll
         for (int m = 0; m < (1 << lvl); ++m) cand[m] = b[s - 1 + 2 * s * m];
         // candidate m = sum_q p[q] 2^(lvl - 1 - q): reduce by the last outcome first
@@ -294,6 +296,266 @@ __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
     }
 }
 
+// ------------------------------------------------------------------ matrix-core encoder
+// The same encoder with its three D x D matrix-vector products on the fp32 matrix cores:
+// v_mfma_f32_16x16x4_f32 adds the four products of its k = 0..3 to the accumulator one
+// after another, each with one rounding (an fma chain in k order), so a chain of 32 of them
+// over k-steps s = 0..31 covering d = 4s + k is the fma chain d = 0..127 above, bit for bit,
+// denormals and signed zeros included.  The norms come out of the same instruction: with
+// both operands equal to the tile of vectors, the diagonal of the 16 x 16 product is each
+// vector's own fma chain of x_d * x_d.
+//
+// A wave encodes a tile of 16 vectors at a time.  Lane l = 16 g + v (v = l % 16, g = l / 16)
+// holds element 4s + g of vector v for s = 0..31: that is the B operand (k = g, column v) of
+// every product, and a product's accumulator comes back to the lanes of its column v, so a
+// vector never leaves its four lanes.  The matrices are the A operands, read from an LDS
+// image laid out per (16-row tile t, k-step block sb): 64 lanes x 4 consecutive k-steps, one
+// 16-byte read per lane per block, lane slots xor-swizzled (slot = l ^ (l >> 4)) so that
+// the transposed 4-byte reads of the Q_prod residual stage are bank-conflict free as well.
+//
+// Which output index a row m = 4q + i of tile t computes is a free choice (each output is
+// its own chain); it sets which lane ends up holding it:
+//   CONTIG  (Q_mse codes, QJL signs): index 32q + 4t + i -> lane g holds [32g, 32g + 32),
+//           packed and stored by that lane directly;
+//   STRIDED (Q_prod codes): index 4(4t + i) + q -> lane g holds the indices 4s + g, the
+//           B-operand layout of the residual decode that consumes them; one LDS round trip
+//           regroups them for packing.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int MQ_WAVES = 8;                 // waves per workgroup, each on its own tiles
+constexpr int MQ_THREADS = 64 * MQ_WAVES;
+constexpr int64_t MQ_MIN_VECTORS = 4096;    // below this the lane-per-vector kernel is used
+
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// LDS image of the D x D matrix M (row = output index, column = d) for A-operand reads.
+template <bool STRIDED>
+__device__ __forceinline__ void build_image(float* img, const float* __restrict__ M) {
+    for (int idx = threadIdx.x; idx < D * D / 4; idx += MQ_THREADS) {
+        const int row = idx >> 5, s = idx & 31;  // columns 4s .. 4s + 3
+        const float4 val = reinterpret_cast<const float4*>(M)[idx];
+        int t, q, i;
+        if (STRIDED) {
+            t = row >> 4, i = (row >> 2) & 3, q = row & 3;
+        } else {
+            q = row >> 5, t = (row >> 2) & 7, i = row & 3;
+        }
+        const int m = 4 * q + i;
+        float* blk = img + (t * 8 + (s >> 2)) * 256 + (s & 3);
+        const float e[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) blk[4 * ((16 * k + m) ^ k)] = e[k];
+    }
+}
+
+// The 16 diagonal entries of a Gram accumulator (lane 16 g + v, register i holds row 4g + i,
+// column v), returned to every lane of column v.
+__device__ __forceinline__ float gram_diag(const f32x4& acc, int v) {
+    const int r = v & 3;
+    const float mine = r == 0 ? acc[0] : r == 1 ? acc[1] : r == 2 ? acc[2] : acc[3];
+    return __shfl(mine, v + 16 * (v >> 2));
+}
+
+// Rotation / QJL products of one tile: acc[t][i] = chain over d of b[d] * M[row(t, 4g + i)][d],
+// with b held as described above (b[s] = element 4s + g) and `a` this lane's slot of image M.
+__device__ __forceinline__ void image_products(const float4* __restrict__ a, const float* b, f32x4* acc) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // two register sets of A values: block sb + 1 is read while block sb's products run; the
+    // scheduling barriers keep the compiler from hoisting every block's reads to the top
+    float4 cur[8], nxt[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) cur[t] = a[t * 8 * 64];
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+        if (sb + 1 < 8) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) nxt[t] = a[(t * 8 + sb + 1) * 64];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float ae = e == 0 ? cur[t].x : e == 1 ? cur[t].y : e == 2 ? cur[t].z : cur[t].w;
+                acc[t] = mfma_f32(ae, b[4 * sb + e], acc[t]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) cur[t] = nxt[t];
+    }
+}
+
+template <int BITS>
+__device__ __forceinline__ void store_row(uint8_t* dst, const uint32_t* w) {
+    if constexpr (BITS == 4) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else if constexpr (BITS == 2) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) reinterpret_cast<uint32_t*>(dst)[k] = w[k];
+    }
+}
+
+template <int BITS, bool PROD>
+__global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
+    const uint16_t* __restrict__ x, int heads, int64_t tokens, int64_t n_vec, int64_t x_sb, int64_t x_sh,
+    int64_t x_st, const float* __restrict__ R, const float* __restrict__ centers,
+    const float* __restrict__ boundaries, const float* __restrict__ S, uint8_t* __restrict__ codes,
+    uint16_t* __restrict__ norms, uint8_t* __restrict__ signs, uint16_t* __restrict__ rnorms, int64_t out_cap,
+    int64_t out_offset) {
+    __shared__ float4 s_img[(PROD ? 2 : 1) * D * D / 4];                // R image (+ S image)
+    __shared__ uint32_t s_stage[PROD ? MQ_WAVES * 16 * 4 * 8 : 1];      // Q_prod code regrouping
+    __shared__ float s_cent[PROD ? (1 << BITS) : 1];
+    float* img = reinterpret_cast<float*>(s_img);
+    build_image<PROD>(img, R);
+    if constexpr (PROD) {
+        build_image<false>(img + D * D, S);
+        if (threadIdx.x < (1 << BITS)) s_cent[threadIdx.x] = centers[threadIdx.x];
+    }
+    __syncthreads();  // the only barrier: each wave then works on its own tiles
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int v = lane & 15, g = lane >> 4;
+    // v_perm_b32 selector: bf16 element g of a 4-element group -> high half of an fp32
+    const uint32_t sel = ((2u * g + 1u) << 24) | ((2u * g) << 16) | 0x0c0cu;
+    const float4* a_rot = s_img + (lane ^ g);
+    constexpr int ROW = D * BITS / 8;
+    const int64_t n_tiles = (n_vec + 15) / 16;
+
+    for (int64_t tile = (int64_t)blockIdx.x * MQ_WAVES + wave; tile < n_tiles;
+         tile += (int64_t)gridDim.x * MQ_WAVES) {
+        const int64_t vi = tile * 16 + v;
+        const bool live = vi < n_vec;
+        int64_t slot = 0;
+        float xs[32];  // xs[s] = x[v][4s + g]
+        {
+            uint4 w[16];
+            if (live) {
+                const int64_t t = vi % tokens, gh = vi / tokens;
+                const int64_t h = gh % heads, b = gh / heads;
+                slot = gh * out_cap + out_offset + t;
+                const uint4* x4 = reinterpret_cast<const uint4*>(x + b * x_sb + h * x_sh + t * x_st);
+#pragma unroll
+                for (int c = 0; c < 16; ++c) w[c] = x4[c];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 16; ++c) w[c] = make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                xs[2 * c] = __uint_as_float(__builtin_amdgcn_perm(w[c].y, w[c].x, sel));
+                xs[2 * c + 1] = __uint_as_float(__builtin_amdgcn_perm(w[c].w, w[c].z, sel));
+            }
+        }
+        // ---- norm: Gram diagonal; u = x / n
+        f32x4 gacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 32; ++s) gacc = mfma_f32(xs[s], xs[s], gacc);
+        float n = tq::sqrt_rn(gram_diag(gacc, v));
+        if (!(n > 0.0f)) n = 1.0f;
+        float u[32];
+#pragma unroll
+        for (int s = 0; s < 32; ++s) u[s] = tq::div_rn(xs[s], n);
+        const uint32_t n16 = tq::f32_to_f16(n);
+        if (live && g == 0) norms[slot] = (uint16_t)n16;
+
+        // ---- rotation and codes
+        f32x4 acc[8];
+        image_products(a_rot, u, acc);
+        uint32_t out[BITS];
+        BitWriter bw;
+        if constexpr (!PROD) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) bw.put(bucket_search<BITS>(acc[t][i], boundaries), BITS, out);
+            if (live) store_row<BITS>(codes + slot * ROW + 4 * BITS * g, out);
+        } else {
+            // codes of indices 4s + g; regroup through LDS into [32g, 32g + 32) for packing
+            uint32_t cw[8];
+            float cv[32];  // C[code] of index 4s + g: the residual decode's B operand
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cw[k] = 0u;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int s = 4 * t + i;
+                    const uint32_t c = bucket_search<BITS>(acc[t][i], boundaries);
+                    cw[s >> 2] |= c << (8 * (s & 3));
+                    cv[s] = s_cent[c];
+                }
+            uint32_t* stg = s_stage + wave * (16 * 4 * 8);
+            uint4* st4 = reinterpret_cast<uint4*>(stg + (v * 4 + g) * 8);
+            st4[0] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+            st4[1] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+            // the wave's LDS accesses complete in issue order; keep the compiler from moving
+            // the reads above the writes (or the next tile's writes above these reads)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            uint2 rd[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) rd[q] = reinterpret_cast<const uint2*>(stg + (v * 4 + q) * 8)[g];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t wd = a < 4 ? rd[q].x : rd[q].y;
+                    bw.put((wd >> (8 * (a & 3))) & 0xFFu, BITS, out);
+                }
+            if (live) store_row<BITS>(codes + slot * ROW + 4 * BITS * g, out);
+
+            // ---- residual decode khat = C[code] @ R: A = R transposed, read from the STRIDED
+            // image 4 bytes at a time; output row 4g + i of tile t is dim 4(4t + i) + g
+            const int qv = v >> 2, iv = v & 3;
+            int off[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) off[c] = 4 * (16 * qv + 4 * g + (c ^ qv)) + iv;
+            f32x4 kacc[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) kacc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int sp = 0; sp < 32; ++sp)
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    kacc[t] = mfma_f32(img[((sp >> 2) * 8 + t) * 256 + off[sp & 3]], cv[sp], kacc[t]);
+            const float nf = tq::f16_to_f32(n16);
+            float r[32];
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int s = 4 * t + i;
+                    r[s] = xs[s] - tq::bf16_to_f32(tq::f32_to_bf16(kacc[t][i] * nf));
+                }
+            f32x4 racc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < 32; ++s) racc = mfma_f32(r[s], r[s], racc);
+            float rho = tq::sqrt_rn(gram_diag(racc, v));
+            if (!(rho > 0.0f)) rho = 1.0f;
+#pragma unroll
+            for (int s = 0; s < 32; ++s) r[s] = tq::div_rn(r[s], rho);
+            if (live && g == 0) rnorms[slot] = (uint16_t)tq::f32_to_f16(rho);
+
+            // ---- QJL signs of rhat @ S^T (CONTIG image): lane g holds signs [32g, 32g + 32)
+            f32x4 pacc[8];
+            image_products(a_rot + D * D / 4, r, pacc);
+            uint32_t sb = 0u;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sb |= (pacc[t][i] >= 0.0f ? 1u : 0u) << (4 * t + i);
+            if (live) reinterpret_cast<uint32_t*>(signs + slot * (D / 8))[g] = sb;
+        }
+    }
+}
+
 // ------------------------------------------------------------------- dequantise
 // out = bf16((C[code] @ R) * f32(norm)); with QJL (keys of Q_prod) the reference's
 // correction is added in bf16: corr = bf16(((s @ S) * rnorm) * sqrt(pi/2)/D),
@@ -380,8 +642,35 @@ int check_common(const uint16_t* x, int batch, int heads, int64_t tokens, int di
     return TQ_OK;
 }
 
+// Workgroups of the matrix-core encoder that fit on the device at once (each loops over
+// tiles, so more would only repeat the LDS image set-up).
+template <int BITS, bool PROD>
+int64_t resident_groups() {
+    static int64_t cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, quantize_mfma_kernel<BITS, PROD>, MQ_THREADS,
+                                                         0) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        cached[dev] = (int64_t)cus * per_cu;
+    }
+    return cached[dev];
+}
+
 template <int BITS, bool PROD>
 int launch_quantize(const QuantArgs& a, hipStream_t s) {
+    if (a.n_vec >= MQ_MIN_VECTORS) {
+        const int64_t tiles = (a.n_vec + 15) / 16;
+        const int64_t groups = std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, resident_groups<BITS, PROD>());
+        hipLaunchKernelGGL((quantize_mfma_kernel<BITS, PROD>), dim3((unsigned)groups), dim3(MQ_THREADS), 0, s, a.x,
+                           a.heads, a.tokens, a.n_vec, a.x_sb, a.x_sh, a.x_st, a.R, a.centers, a.boundaries, a.S,
+                           a.codes, a.norms, a.signs, a.rnorms, a.out_cap, a.out_offset);
+        TQ_CHECK_LAUNCH();
+        return TQ_OK;
+    }
     const int64_t blocks = (a.n_vec + QBLOCK - 1) / QBLOCK;
     if (blocks == 0) return TQ_OK;
     hipLaunchKernelGGL((quantize_kernel<BITS, PROD>), dim3((unsigned)blocks), dim3(QBLOCK), 0, s, a.x, a.heads,
