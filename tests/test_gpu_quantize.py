@@ -132,6 +132,38 @@ def test_quantize_prod_matrix_core_bit_exact(cuda, bits):
         assert int(t[:, :, :off].count_nonzero()) == 0 and int(t[:, :, off + n:].count_nonzero()) == 0
 
 
+@pytest.mark.parametrize("irregular", ["repeated", "outlying", "unsorted"])
+def test_quantize_mse_matrix_core_irregular_boundaries(cuda, irregular):
+    """Boundary sets the uniform bucketize grid does not cover (a repeated boundary, one far
+    outside the others, an unsorted pair) go through the binary search; codes still equal the
+    oracle's #{b < z}.  For the unsorted set the search no longer counts (it assumes order),
+    so only its own determinism is checked there."""
+    x = _matrix_core_input(cuda, 77)
+    base = layer_codecs(D, 4, 0, False, cuda).value
+    b = base.boundaries.clone()
+    if irregular == "repeated":
+        b[8] = b[7]
+    elif irregular == "outlying":
+        b[14] = 1.0e3
+    else:
+        b[3], b[4] = base.boundaries[4], base.boundaries[3]
+    codec = K.CodecParams(bits=4, rotation=base.rotation, centers=base.centers, boundaries=b)
+    B, H, n, _ = x.shape
+    codes = torch.zeros(B, H, n, 64, dtype=torch.uint8, device=cuda)
+    norms = torch.zeros(B, H, n, dtype=torch.float16, device=cuda)
+    K.quantize_mse(x, codec, codes, norms)
+    torch.cuda.synchronize()
+    if irregular == "unsorted":
+        again = torch.zeros_like(codes)
+        K.quantize_mse(x, codec, again, norms)
+        assert torch.equal(codes, again)
+        return
+    rc, rn = O.encode_mse(u16(x).reshape(-1, D), 4, base.rotation.cpu().numpy(), b.cpu().numpy())
+    got = codes.cpu().numpy().reshape(rc.shape)
+    assert np.array_equal(got, rc), f"{(got != rc).sum()} code bytes differ"
+    assert np.array_equal(u16(norms).reshape(-1), rn)
+
+
 def test_quantize_strided_input_and_decode_append(cuda):
     """A [B,T,H,D] buffer viewed as [B,H,T,D] (HF layout), appended one token at a time."""
     base = kv_bf16((1, 4, 40, D), seed=7, device=cuda)  # [B, T=4?]

@@ -19,6 +19,7 @@
 // :148-154 (_pack_qjl_signs).
 
 #include <algorithm>
+#include <type_traits>
 
 #include "tq_common.h"
 
@@ -324,9 +325,86 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int MQ_WAVES = 8;                 // waves per workgroup, each on its own tiles
 constexpr int MQ_THREADS = 64 * MQ_WAVES;
 constexpr int64_t MQ_MIN_VECTORS = 4096;    // below this the lane-per-vector kernel is used
+constexpr int LUT_MAX = 512;                // cells of the bucketize grid
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// floor(n / d) = (n * m) >> s for 0 <= n < 2^31 and 1 <= d < 2^31, with l = ceil(log2 d),
+// s = 31 + l and m = ceil(2^s / d) < 2^32: then 2^s <= m d <= 2^s + 2^l (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994, Theorem 4.2).
+struct FastDiv {
+    uint32_t m, s;
+};
+FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    return {(uint32_t)(((1ull << (31 + l)) + d - 1) / d), 31 + l};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+    return (uint32_t)(((uint64_t)n * f.m) >> f.s);
+}
+
+// ---- bucketize through a uniform grid
+// code(z) = #{i : b_i < z} for the NB sorted boundaries.  Cells of width w = (smallest gap
+// between neighbouring boundaries) / 4 start at e0 = b_0 - 2w; cell k stores
+// c0 = #{i : b_i < e0 + (k - 1) w} and b_{c0} (+inf when c0 = NB).  z goes to the cell
+// k = clamp(floor((z - e0) / w), 0, cells - 1), and code(z) = c0 + [b_{c0} < z].  Exact, not
+// approximate: the computed (z - e0) / w is within 1e-3 of the real quotient (both |e0| / w and
+// |b_NB-1| / w are kept below 4096), so e0 + (k - 1) w < z < e0 + (k + 2) w, a window of 3w
+// that holds no two boundaries (the gap is 4w).  Every b_i below the window's start is < z,
+// b_{c0 + 1} >= b_{c0} + 4w is above its end, and b_{c0} decides the rest.  The two clamped
+// ends: k = 0 covers z < b_0 - w and NaN (c0 = 0, [b_0 < z] false), and the last cell starts
+// more than w above b_NB-1 (c0 = NB).  A boundary set without that geometry (unsorted,
+// repeated, or too many cells) uses bucket_search instead.
+struct BucketGrid {
+    float scale, offset, top;  // f = z * scale + offset; cells = top + 1
+    float w, e0;
+    int cells;
+    bool ok;
+};
+template <int NB>
+__device__ __forceinline__ BucketGrid bucket_grid(const float* __restrict__ b) {
+    BucketGrid g{0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0, false};
+    if constexpr (NB > 1) {
+        float gap = b[1] - b[0];
+        bool sorted = gap > 0.0f;
+#pragma unroll
+        for (int i = 2; i < NB; ++i) {
+            const float d = b[i] - b[i - 1];
+            sorted = sorted && d > 0.0f;
+            gap = fminf(gap, d);
+        }
+        const float w = gap * 0.25f;
+        const float e0 = b[0] - 2.0f * w;
+        const float span = (b[NB - 1] - e0) / w;
+        g.w = w;
+        g.e0 = e0;
+        g.scale = 1.0f / w;
+        g.offset = -e0 * g.scale;
+        g.ok = sorted && w > 0.0f && span < (float)(LUT_MAX - 5) && fabsf(g.offset) < 4096.0f &&
+               fabsf(b[NB - 1] * g.scale) < 4096.0f;
+        g.cells = g.ok ? (int)ceilf(span) + 4 : 0;
+        g.top = (float)(g.cells - 1);
+    }
+    return g;
+}
+template <int NB>
+__device__ __forceinline__ void fill_bucket_grid(float2* lut, const BucketGrid& g, const float* __restrict__ b) {
+    for (int k = threadIdx.x; k < g.cells; k += MQ_THREADS) {
+        const float start = g.e0 + (float)(k - 1) * g.w;
+        uint32_t c0 = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) c0 += b[i] < start ? 1u : 0u;
+        lut[k] = make_float2(c0 < NB ? b[c0] : __builtin_inff(), __uint_as_float(c0));
+    }
+}
+__device__ __forceinline__ uint32_t bucket_lookup(float z, const float2* lut, const BucketGrid& g) {
+    float f = __builtin_fmaf(z, g.scale, g.offset);
+    f = fminf(fmaxf(f, 0.0f), g.top);  // NaN -> 0
+    const float2 e = lut[(uint32_t)f];
+    return __float_as_uint(e.y) + (e.x < z ? 1u : 0u);
 }
 
 // LDS image of the D x D matrix M (row = output index, column = d) for A-operand reads.
@@ -405,10 +483,15 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
     int64_t x_st, const float* __restrict__ R, const float* __restrict__ centers,
     const float* __restrict__ boundaries, const float* __restrict__ S, uint8_t* __restrict__ codes,
     uint16_t* __restrict__ norms, uint8_t* __restrict__ signs, uint16_t* __restrict__ rnorms, int64_t out_cap,
-    int64_t out_offset) {
+    int64_t out_offset, FastDiv tok_div, FastDiv head_div) {
     __shared__ float4 s_img[(PROD ? 2 : 1) * D * D / 4];                // R image (+ S image)
     __shared__ uint32_t s_stage[PROD ? MQ_WAVES * 16 * 4 * 8 : 1];      // Q_prod code regrouping
     __shared__ float s_cent[PROD ? (1 << BITS) : 1];
+    constexpr int NB = (1 << BITS) - 1;
+    __shared__ float2 s_lut[NB > 1 ? LUT_MAX : 1];
+    const BucketGrid grid = bucket_grid<NB>(boundaries);
+    const bool use_grid = __builtin_amdgcn_readfirstlane(grid.ok ? 1 : 0) != 0;
+    if (NB > 1 && use_grid) fill_bucket_grid<NB>(s_lut, grid, boundaries);
     float* img = reinterpret_cast<float*>(s_img);
     build_image<PROD>(img, R);
     if constexpr (PROD) {
@@ -427,17 +510,18 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
 
     for (int64_t tile = (int64_t)blockIdx.x * MQ_WAVES + wave; tile < n_tiles;
          tile += (int64_t)gridDim.x * MQ_WAVES) {
-        const int64_t vi = tile * 16 + v;
-        const bool live = vi < n_vec;
+        const uint32_t vi = (uint32_t)tile * 16u + (uint32_t)v;  // n_vec < 2^31
+        const bool live = vi < (uint64_t)n_vec;
         int64_t slot = 0;
         float xs[32];  // xs[s] = x[v][4s + g]
         {
             uint4 w[16];
             if (live) {
-                const int64_t t = vi % tokens, gh = vi / tokens;
-                const int64_t h = gh % heads, b = gh / heads;
-                slot = gh * out_cap + out_offset + t;
-                const uint4* x4 = reinterpret_cast<const uint4*>(x + b * x_sb + h * x_sh + t * x_st);
+                const uint32_t gh = fdiv(vi, tok_div), t = vi - gh * (uint32_t)tokens;
+                const uint32_t b = fdiv(gh, head_div), h = gh - b * (uint32_t)heads;
+                slot = (int64_t)gh * out_cap + out_offset + t;
+                const uint4* x4 =
+                    reinterpret_cast<const uint4*>(x + (int64_t)b * x_sb + (int64_t)h * x_sh + (int64_t)t * x_st);
 #pragma unroll
                 for (int c = 0; c < 16; ++c) w[c] = x4[c];
             } else {
@@ -467,11 +551,20 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
         image_products(a_rot, u, acc);
         uint32_t out[BITS];
         BitWriter bw;
+        auto code_of = [&](float z, auto grid_path) -> uint32_t {
+            if constexpr (NB == 1) return boundaries[0] < z ? 1u : 0u;
+            else if constexpr (decltype(grid_path)::value) return bucket_lookup(z, s_lut, grid);
+            else return bucket_search<BITS>(z, boundaries);
+        };
         if constexpr (!PROD) {
+            auto pack = [&](auto grid_path) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
+                for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) bw.put(bucket_search<BITS>(acc[t][i], boundaries), BITS, out);
+                    for (int i = 0; i < 4; ++i) bw.put(code_of(acc[t][i], grid_path), BITS, out);
+            };
+            if (use_grid) pack(std::true_type{});
+            else pack(std::false_type{});
             if (live) store_row<BITS>(codes + slot * ROW + 4 * BITS * g, out);
         } else {
             // codes of indices 4s + g; regroup through LDS into [32g, 32g + 32) for packing
@@ -479,15 +572,19 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
             float cv[32];  // C[code] of index 4s + g: the residual decode's B operand
 #pragma unroll
             for (int k = 0; k < 8; ++k) cw[k] = 0u;
+            auto codes_of = [&](auto grid_path) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
+                for (int t = 0; t < 8; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int s = 4 * t + i;
-                    const uint32_t c = bucket_search<BITS>(acc[t][i], boundaries);
-                    cw[s >> 2] |= c << (8 * (s & 3));
-                    cv[s] = s_cent[c];
-                }
+                    for (int i = 0; i < 4; ++i) {
+                        const int s = 4 * t + i;
+                        const uint32_t c = code_of(acc[t][i], grid_path);
+                        cw[s >> 2] |= c << (8 * (s & 3));
+                        cv[s] = s_cent[c];
+                    }
+            };
+            if (use_grid) codes_of(std::true_type{});
+            else codes_of(std::false_type{});
             uint32_t* stg = s_stage + wave * (16 * 4 * 8);
             uint4* st4 = reinterpret_cast<uint4*>(stg + (v * 4 + g) * 8);
             st4[0] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
@@ -520,11 +617,30 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
             f32x4 kacc[8];
 #pragma unroll
             for (int t = 0; t < 8; ++t) kacc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            // k-step block sb covers s' = 4 sb + e; its 32 A values are read one block ahead
+            float ka[8][4], kn[8][4];
 #pragma unroll
-            for (int sp = 0; sp < 32; ++sp)
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ka[t][e] = img[t * 256 + off[e]];
+#pragma unroll
+            for (int sb = 0; sb < 8; ++sb) {
+                if (sb + 1 < 8) {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) kn[t][e] = img[((sb + 1) * 8 + t) * 256 + off[e]];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) kacc[t] = mfma_f32(ka[t][e], cv[4 * sb + e], kacc[t]);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
-                    kacc[t] = mfma_f32(img[((sp >> 2) * 8 + t) * 256 + off[sp & 3]], cv[sp], kacc[t]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ka[t][e] = kn[t][e];
+            }
             const float nf = tq::f16_to_f32(n16);
             float r[32];
 #pragma unroll
@@ -662,12 +778,13 @@ int64_t resident_groups() {
 
 template <int BITS, bool PROD>
 int launch_quantize(const QuantArgs& a, hipStream_t s) {
-    if (a.n_vec >= MQ_MIN_VECTORS) {
+    if (a.n_vec >= MQ_MIN_VECTORS && a.n_vec < ((int64_t)1 << 31)) {
         const int64_t tiles = (a.n_vec + 15) / 16;
         const int64_t groups = std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, resident_groups<BITS, PROD>());
         hipLaunchKernelGGL((quantize_mfma_kernel<BITS, PROD>), dim3((unsigned)groups), dim3(MQ_THREADS), 0, s, a.x,
                            a.heads, a.tokens, a.n_vec, a.x_sb, a.x_sh, a.x_st, a.R, a.centers, a.boundaries, a.S,
-                           a.codes, a.norms, a.signs, a.rnorms, a.out_cap, a.out_offset);
+                           a.codes, a.norms, a.signs, a.rnorms, a.out_cap, a.out_offset,
+                           make_fastdiv((uint32_t)a.tokens), make_fastdiv((uint32_t)a.heads));
         TQ_CHECK_LAUNCH();
         return TQ_OK;
     }
