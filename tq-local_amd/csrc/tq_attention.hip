@@ -58,10 +58,18 @@ constexpr int D = TQ_DIM;
 #ifndef TQ_ATTN_WAVES_G8
 #define TQ_ATTN_WAVES_G8 12
 #endif
+#ifndef TQ_ATTN_SETS_G4
+#define TQ_ATTN_SETS_G4 2
+#endif
+#ifndef TQ_ATTN_SETS_G8
+#define TQ_ATTN_SETS_G8 2
+#endif
 template <int VB, int GC, bool QJL>
 struct Cfg {
     static constexpr int NW = GC == 1 ? ((VB == 3 && QJL) ? 12 : TQ_ATTN_WAVES_G4) : (VB == 3 ? 8 : TQ_ATTN_WAVES_G8);
     static constexpr int NT = NW * 64;
+    // per-wave blocks in flight (register sets of packed data)
+    static constexpr int NSET = GC == 1 ? TQ_ATTN_SETS_G4 : TQ_ATTN_SETS_G8;
 };
 constexpr int BLK = 16;        // tokens per block (MFMA N)
 // lane-private copies of the key pair table: 32 for the 64-entry (3-bit) table; the 256-entry
@@ -407,9 +415,12 @@ __device__ __forceinline__ void build_image(const uint16_t* __restrict__ q, int 
     const int b = grp / kv_heads, kvh = grp - b * kv_heads;
     const int bh0 = b * q_heads + kvh * G;
 
-    for (int i = tid; i < NH * D; i += NTH) {
-        const int h = i / D, d = i % D;
-        L.qs[h][d] = h < G ? tq::bf16_to_f32(q[(size_t)(bh0 + h) * D + d]) : 0.0f;
+    constexpr int QPT = (NH * D + NTH - 1) / NTH;  // query values per thread
+    uint32_t qv[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = tid + k * NTH, h = i / D, d = i % D;
+        qv[k] = (i < NH * D && h < G) ? (uint32_t)q[(size_t)(bh0 + h) * D + d] : 0u;
     }
     constexpr int MATS = QJL ? 2 : 1;
     const bool mv_thread = tid < MATS * 2 * D;
@@ -419,6 +430,11 @@ __device__ __forceinline__ void build_image(const uint16_t* __restrict__ q, int 
         const float4* row = reinterpret_cast<const float4*>((mat ? S : Rk) + (size_t)j * D) + 16 * hf;
 #pragma unroll
         for (int i = 0; i < 16; ++i) r4[i] = row[i];
+    }
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = tid + k * NTH;
+        if (i < NH * D) L.qs[i / D][i % D] = tq::bf16_to_f32(qv[k]);
     }
     __syncthreads();
     if (mv_thread) {
@@ -616,6 +632,21 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             }
         }
     };
+
+    // blocks of this wave: wave, wave + NW, ... (scalar count)
+    const int first = wave * BLK;
+    const int nb = first < nt ? (nt - first + STEP - 1) / STEP : 0;
+    // NSET of this wave's blocks in flight: block i is processed from register set i mod NSET,
+    // which is then refilled with block i + NSET, so the sets rotate without copies and a load
+    // has NSET - 1 blocks of processing to arrive in.  The refills are unconditional (past the
+    // range the buffer loads return zeros and read no memory): with a load count that depends
+    // on the path, the compiler's counter waits assume the fewest loads outstanding and block
+    // i's first wait would also wait for block i + 1.  For the same reason the load order is
+    // pinned with scheduling barriers here as in the loop: the waits at the loop head hold for
+    // both ways in, and first loads issued in another order would force a wait for all of them.
+    constexpr int NSET = Cfg<VB, GC, QJL>::NSET;
+    Kd kset[NSET];
+    Vd vset[NSET];
 
     // ------------------------------------------------------------ prologue
     // phase 1: codebooks (hi|lo) and the group's q-side image (every split workgroup of the
@@ -910,14 +941,12 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         __builtin_amdgcn_s_setprio(0);
     };
 
-    // blocks of this wave: wave, wave + NW, ... (scalar count)
-    const int first = wave * BLK;
-    const int nb = first < nt ? (nt - first + STEP - 1) / STEP : 0;
+#pragma unroll
+    for (int s = 0; s < NSET; ++s) {
+        load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     if (nb > 0) {
-        // two of this wave's blocks in flight: while one is processed the next-but-one is
-        // loaded into the register set just consumed, so A and B alternate without copies
-        Kd ka, kb;
-        Vd va, vb;
         auto process = [&](const Kd& K_, const Vd& V_, int rel) {
             float lg[R::HPL];
             if (scores(K_, rel, lg)) raise_max(lg);
@@ -925,19 +954,19 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             weights(lg, K_.vn, av);
             values(V_, av);
         };
-        int rel = first;
-        load_k(ka, rel);
-        load_v(va, rel);
-        if (nb > 1) load_k(kb, rel + STEP), load_v(vb, rel + STEP);
-        int i = 0;
-        for (; i + 2 <= nb; i += 2) {
-            process(ka, va, rel);
-            if (i + 2 < nb) load_k(ka, rel + 2 * STEP), load_v(va, rel + 2 * STEP);
-            process(kb, vb, rel + STEP);
-            if (i + 3 < nb) load_k(kb, rel + 3 * STEP), load_v(vb, rel + 3 * STEP);
-            rel += 2 * STEP;
+        // whole rounds of NSET blocks, also without a branch around each block: up to NSET - 1
+        // blocks past the range are processed (all their tokens are masked, weights 0; the
+        // wave's first block was in range, so the reference maximum is finite by then)
+        for (int i = 0; i < nb; i += NSET) {
+#pragma unroll
+            for (int s = 0; s < NSET; ++s) {
+                const int rel = first + (i + s) * STEP;
+                process(kset[s], vset[s], rel);
+                __builtin_amdgcn_sched_barrier(0);
+                load_k(kset[s], rel + NSET * STEP), load_v(vset[s], rel + NSET * STEP);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        if (i < nb) process(ka, va, rel);
     }
 
     // ------------------------------------------------------------ epilogue
