@@ -73,7 +73,7 @@ struct Cfg {
 };
 constexpr int BLK = 16;        // tokens per block (MFMA N)
 // lane-private copies of the key pair table: 32 for the 64-entry (3-bit) table; the 256-entry
-// 4-bit table gets 8 where the paired value table already takes 64 KB of LDS
+// 4-bit table gets 8 where the value pair table already takes 64 KB of LDS
 template <int KB, bool PV>
 constexpr int KCOPIES = KB <= 3 ? 32 : (PV ? 8 : 32);
 constexpr int WT_STRIDE = 20;  // dwords per row of the weight-transpose buffer (bank spread)
@@ -231,6 +231,12 @@ struct Rows {
 // and the A operand is zero where the parities differ.
 template <int VB, int GC>
 constexpr bool PAIRED = GC == 1 && (VB == 4 || VB == 3);
+// Pair-table lookups in the generic layout (5..8 heads, 3- and 4-bit values): lane n's code
+// byte (4-bit) or 6-bit field (3-bit) of dims 8 n + 2 b, 8 n + 2 b + 1 is looked up once, and
+// the two values feed the MFMAs of dims 8 n + 2 b (even) and 8 n + 2 b + 1 (odd), whose
+// column n they both are: half the lookups of one per code, the same MFMAs.
+template <int VB, int GC>
+constexpr bool PAIR_COLS = GC == 2 && (VB == 4 || VB == 3);
 constexpr int VCOPIES = 32;      // lane-private copies of the pair table (bank pair per lane)
 constexpr int WT_STRIDE_P = 36;  // dwords per weight row in the paired layout (32 slots + bank spread)
 
@@ -251,15 +257,16 @@ struct Smem {
     static constexpr int NH = 4 * GC;
     static constexpr int NW = Cfg<VB, GC, QJL>::NW;
     static constexpr bool PV = PAIRED<VB, GC>;
+    static constexpr bool PT = PV || PAIR_COLS<VB, GC>;  // the pair table is built
     static constexpr int WTS = PV ? WT_STRIDE_P : WT_STRIDE;
     // both lookup tables sit below 64 KB, so their base folds into the LDS instruction's offset.
     // (Ck hi|lo of c0, Ck hi|lo of c1) per pair of key codes; KC lane-private copies, entry e of
     // copy c at byte 8 (KC e + c), so the lanes of a 32-lane LDS pass use distinct bank pairs
-    static constexpr int KC = KCOPIES<KB, PV>;
+    static constexpr int KC = KCOPIES<KB, PT>;
     uint2 ktab[1 << (2 * KB)][KC];
     // paired: (Cv hi|lo of the even dim's code, Cv hi|lo of the odd dim's code) per pair of
     // codes (2^(2 VB) entries), entry e of copy c at byte 256 e + 8 c from the table base
-    uint2 vtab2[PV ? (1 << (2 * VB)) : 1][PV ? VCOPIES : 1];
+    uint2 vtab2[PT ? (1 << (2 * VB)) : 1][PT ? VCOPIES : 1];
     uint32_t vtab[1 << VB];             // Cv hi|lo per value code (generic layout)
     uint32_t wt[NW][16][WTS];           // per-wave transpose of the softmax weights
     union {
@@ -664,7 +671,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         const int e = i / Sm::KC;
         (&sm.ktab[0][0])[i] = make_uint2(sm.u.pro.ksrc[e & ((1 << KB) - 1)], sm.u.pro.ksrc[e >> KB]);
     }
-    if constexpr (Sm::PV) {
+    if constexpr (Sm::PT) {
         for (int i = tid; i < (1 << (2 * VB)) * VCOPIES; i += NT) {
             const int e = i / VCOPIES;
             (&sm.vtab2[0][0])[i] = make_uint2(sm.vtab[e & ((1 << VB) - 1)], sm.vtab[e >> VB]);
@@ -896,6 +903,34 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                     const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
                     acc_v[m] = mfma_bf16(av.a[u], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
                 }
+            }
+        } else if constexpr (PAIR_COLS<VB, GC>) {
+            // generic layout, one pair-table lookup per two codes: lane (n, g) supplies tokens
+            // 4 r + g (k-slots 8 g + 2 r + y); pair b of its 8-dim chunk feeds MFMAs 2 b and 2 b + 1
+            uint32_t ch[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (VB == 3)
+                    ch[r] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh) : B.vw[r][1] >> (vsh - 32);
+                else
+                    ch[r] = B.vw[r][0];
+            }
+#pragma unroll
+            for (int pb = 0; pb < 4; ++pb) {
+                uint2 e[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    uint32_t o;
+                    if constexpr (VB == 4) {
+                        // LDS byte offset 256 * byte pb + plane in one v_perm: [plane, byte pb, 0, 0]
+                        o = __builtin_amdgcn_perm(ch[r], plane, 0x0C0C0000u | ((4u + (uint32_t)pb) << 8));
+                    } else {
+                        o = field_x<6, 8>(&ch[r], 6 * pb) | plane;
+                    }
+                    e[r] = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o);
+                }
+                acc_v[2 * pb] = mfma_bf16(av.a[0], u32x4{e[0].x, e[1].x, e[2].x, e[3].x}, acc_v[2 * pb]);
+                acc_v[2 * pb + 1] = mfma_bf16(av.a[0], u32x4{e[0].y, e[1].y, e[2].y, e[3].y}, acc_v[2 * pb + 1]);
             }
         } else {
             // lane (n, g) supplies tokens 4 r + g (k-slots 8 g + 2 r + y), dim 8 n + m
