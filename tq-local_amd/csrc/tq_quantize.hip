@@ -545,6 +545,13 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
         for (int s = 0; s < 32; ++s) u[s] = tq::div_rn(xs[s], n);
         const uint32_t n16 = tq::f32_to_f16(n);
         if (live && g == 0) norms[slot] = (uint16_t)n16;
+        // Q_prod: the input elements again at the residual, held as bf16 pairs meanwhile
+        uint32_t xp[PROD ? 16 : 1];
+        if constexpr (PROD) {
+#pragma unroll
+            for (int c = 0; c < 16; ++c)
+                xp[c] = __builtin_amdgcn_perm(__float_as_uint(xs[2 * c + 1]), __float_as_uint(xs[2 * c]), 0x07060302u);
+        }
 
         // ---- rotation and codes
         f32x4 acc[8];
@@ -648,7 +655,8 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int s = 4 * t + i;
-                    r[s] = xs[s] - tq::bf16_to_f32(tq::f32_to_bf16(kacc[t][i] * nf));
+                    const float x = __uint_as_float((s & 1) ? (xp[s >> 1] & 0xFFFF0000u) : (xp[s >> 1] << 16));
+                    r[s] = x - tq::bf16_to_f32(tq::f32_to_bf16(kacc[t][i] * nf));
                 }
             f32x4 racc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
