@@ -86,7 +86,7 @@ size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, int kv_heads,
  * codebook dequant, QJL logit correction, softmax, V accumulation, the
  * cross-split log-sum-exp merge and the final un-rotation by R_v.
  *
- *   q        bf16 [batch][q_heads][dim] (contiguous)
+ *   q        bf16 [batch][q_heads][dim] (contiguous, 16-byte aligned)
  *   seq_starts int32 [batch] first valid token per sequence (nullable: 0), for
  *            left-padded batches
  *   seq_lens int32 [batch] end of the valid tokens per sequence (nullable: n_tokens)

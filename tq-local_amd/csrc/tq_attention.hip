@@ -188,12 +188,10 @@ struct Ws {
 
 // Per-group q-side image, built in LDS by every split workgroup of the group: the register
 // contents of the key-score and QJL A operands for one wave (lane-major, one 16-byte read per
-// lane and slot), the per-head QJL offsets and the fixed-point scale.
-constexpr int IMG_QA = 0;                   // [8 j][64 lanes][4]  key-score A operand
+// lane and slot).
+constexpr int IMG_QA = 0;                    // [8 j][64 lanes][4]  key-score A operand
 constexpr int IMG_QJ = IMG_QA + 8 * 64 * 4;  // [set][2 jj][64 lanes][4]  QJL A operand (int8 limbs)
-constexpr int IMG_SQ = IMG_QJ + 2 * 2 * 64 * 4;  // [8 heads] sum_d q_proj (fixed-point, as float)
-constexpr int IMG_QFIX = IMG_SQ + 8;         // 2^(1 - F)
-constexpr int IMG_DW = IMG_QFIX + 8;         // dwords per group (a multiple of 4)
+constexpr int IMG_DW = IMG_QJ + 2 * 2 * 64 * 4;  // dwords per group (a multiple of 4)
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -244,12 +242,8 @@ constexpr int WT_STRIDE_P = 36;  // dwords per weight row in the paired layout (
 template <int GC>
 struct PrepLds {
     static constexpr int NH = 4 * GC;
-    float qs[NH][D];
-    float qr[NH][D];
-    float qp[NH][D];
-    double sqd[2 * NH];
-    float red[16];
-    uint32_t limb[4][NH][4][8];
+    float qp[NH][D];  // q S^T of the group's heads
+    float red[16];    // max |q S^T| per matrix-core tile
 };
 
 template <int KB, int VB, bool QJL, int GC>
@@ -287,18 +281,23 @@ struct Smem {
 // ----------------------------------------------------------------- merge
 // One query head bh, MT threads (t = 0..MT-1): merge the split partials (maxima in the log2
 // domain), normalise, un-rotate by R_v.  Thread t reads R_v rows k in [16 (t / 32), 16 (t / 32)
-// + 16), columns 4 (t % 32) .. + 3, as float4.  Every thread of the workgroup calls this the
-// same number of times (barriers inside); act = false threads only take part in the barriers.
-__device__ __forceinline__ void merge_head(int bh, bool act, int t, int n_split, const float* __restrict__ part_o,
+// + 16), columns 4 (t % 32) .. + 3, as float4.  Every thread of the workgroup calls it (barriers
+// inside).
+__device__ __forceinline__ void merge_head(int bh, int t, int n_split, const float* __restrict__ part_o,
                                            const float* __restrict__ part_ml, const float* __restrict__ Rv,
                                            float* __restrict__ out_f32, uint16_t* __restrict__ out_bf16,
                                            float* __restrict__ lse_out, float* so, float4 (*part)[D / 4],
                                            float (*red)[2]) {
     const int lane = t & 63, wv = t >> 6;
+    // this thread's slice of R_v, loaded first: its L2 latency overlaps the merge of the splits
+    const int c4 = t & 31, kr = t >> 5;
+    const float4* rv4 = reinterpret_cast<const float4*>(Rv);
+    float4 rvs[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) rvs[i] = rv4[(size_t)(16 * kr + i) * (D / 4) + c4];
     const float* ml = part_ml + (size_t)bh * n_split * 2;
     float M = NEG_INF;
-    if (act)
-        for (int k = t; k < n_split; k += MT) M = fmaxf(M, ml[2 * k]);
+    for (int k = t; k < n_split; k += MT) M = fmaxf(M, ml[2 * k]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
     if (lane == 0) red[wv][0] = M;
@@ -307,7 +306,7 @@ __device__ __forceinline__ void merge_head(int bh, bool act, int t, int n_split,
     // normalised rotated output: threads (half, d) split the splits in two
     const int d = t & (D - 1), hf = t >> 7;
     float o = 0.0f, sacc = 0.0f;
-    if (act && M != NEG_INF) {
+    if (M != NEG_INF) {
         // unrolled so that several splits' loads are in flight together (the fma order is
         // unchanged)
 #pragma unroll 4
@@ -325,17 +324,14 @@ __device__ __forceinline__ void merge_head(int bh, bool act, int t, int n_split,
     if (t < D) {
         const float sum = red[0][1] + red[1][1];
         so[t] = (M != NEG_INF) ? (po2[t] + po2[t + D]) / fmaxf(sum, 1e-8f) : 0.0f;
-        if (act && lse_out && t == 0) lse_out[bh] = (M != NEG_INF) ? M * LN2 + logf(sum) : NEG_INF;
+        if (lse_out && t == 0) lse_out[bh] = (M != NEG_INF) ? M * LN2 + logf(sum) : NEG_INF;
     }
     __syncthreads();
-    const int c4 = t & 31, kr = t >> 5;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4* rv4 = reinterpret_cast<const float4*>(Rv);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int k = 16 * kr + i;
-        const float4 r = rv4[(size_t)k * (D / 4) + c4];
-        const float w = so[k];
+        const float4 r = rvs[i];
+        const float w = so[16 * kr + i];
         acc.x = __builtin_fmaf(w, r.x, acc.x);
         acc.y = __builtin_fmaf(w, r.y, acc.y);
         acc.z = __builtin_fmaf(w, r.z, acc.z);
@@ -344,7 +340,7 @@ __device__ __forceinline__ void merge_head(int bh, bool act, int t, int n_split,
     __syncthreads();  // so / po2 reads above are done before part is overwritten
     part[kr][c4] = acc;
     __syncthreads();
-    if (act && t < D) {
+    if (t < D) {
         const float* pf = reinterpret_cast<const float*>(part);
         float a = 0.0f;
 #pragma unroll
@@ -352,7 +348,6 @@ __device__ __forceinline__ void merge_head(int bh, bool act, int t, int n_split,
         if (out_f32) out_f32[(size_t)bh * D + t] = a;
         if (out_bf16) out_bf16[(size_t)bh * D + t] = (uint16_t)tq::f32_to_bf16(a);
     }
-    __syncthreads();  // scratch reused by the next head
 }
 
 // One workgroup per (batch row, query head).
@@ -363,7 +358,7 @@ __global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ par
     __shared__ float so[D];
     __shared__ float4 part[MT / 32][D / 4];
     __shared__ float red[MT / 64][2];
-    merge_head(blockIdx.x, true, threadIdx.x, n_split, part_o, part_ml, Rv, out_f32, out_bf16, lse_out, so, part, red);
+    merge_head(blockIdx.x, threadIdx.x, n_split, part_o, part_ml, Rv, out_f32, out_bf16, lse_out, so, part, red);
 }
 
 // ------------------------------------------------------------------ q-side image
@@ -374,145 +369,174 @@ __global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ par
 //              R::row(h, x), x = 0: bf16(q_rot), x = 1: bf16(q_rot - bf16(q_rot));
 //   QJL:       x_d = rint(q_proj_d 2^(G2 - d % 8)) (negated for d % 8 = 7) in four balanced
 //              base-256 digits (int8 limbs), rows (head, limb), byte e of VGPR v of MFMA jj <->
-//              dim 32 g + 4 jj + v + 8 e; sum_d y_d (y_d = x_d 2^(d % 8), exact) per head and
-//              2^(1 - G2), both times the QJL logit scale.  The key-score operand carries the
-//              logit scale times log2 e.
-// Balanced base-256 digits of x (|x| < 2^29) into the limb image lb[limb][head][d / 32][d % 8]
-// byte (d / 8) % 4.
-template <int NH>
-__device__ __forceinline__ void put_limbs(uint8_t* lb, int h, int d, int x) {
-    const int gg = d >> 5, sh = d & 7, e8 = (d >> 3) & 3;
+//              dim 32 g + 4 jj + v + 8 e.  The key-score operand carries the logit scale times
+//              log2 e; the QJL scale 2^(1 - G2) times the QJL logit scale is applied per token.
+//
+// The mat-vecs run on the matrix cores, one 16-column tile per wave: tile t < 8 is columns
+// [16 t, 16 t + 16) of q R_k^T, tile t >= 8 the same columns of q S^T.  A = q (rows = query
+// heads, bf16 as given, exact); B = the matrix rows, each fp32 element split exactly into three
+// bf16 terms hi + mid + lo (truncations: hi keeps the top 8 significant bits, mid the next 8,
+// and the rest has at most 8), so every product is exact and the sums are fp32 MFMA
+// accumulations.  Lane (c, kq) reads 32 bytes of each of rows 16 t + c per k-step: 16 rows per
+// load instruction instead of one row per lane.
+
+// hi | mid | lo bf16 terms of the 8 floats of one lane's k-step (element e <-> k-slot e)
+__device__ __forceinline__ void split3_bf16(const float4& a, const float4& b, u32x4& hi, u32x4& mid, u32x4& lo) {
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int l = ((x + 128) & 255) - 128;
-        lb[(((k * NH + h) * 4 + gg) * 8 + sh) * 4 + e8] = (uint8_t)(l & 255);
-        x = (x - l) >> 8;
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t x0 = __float_as_uint(x[2 * p]), x1 = __float_as_uint(x[2 * p + 1]);
+        hi[p] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+        const float r0 = x[2 * p] - __uint_as_float(x0 & 0xFFFF0000u);
+        const float r1 = x[2 * p + 1] - __uint_as_float(x1 & 0xFFFF0000u);
+        const uint32_t u0 = __float_as_uint(r0), u1 = __float_as_uint(r1);
+        mid[p] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+        const float l0 = r0 - __uint_as_float(u0 & 0xFFFF0000u);
+        const float l1 = r1 - __uint_as_float(u1 & 0xFFFF0000u);
+        lo[p] = __builtin_amdgcn_perm(__float_as_uint(l1), __float_as_uint(l0), 0x07060302u);
     }
 }
 
-// Block-wide max of |v| over NH * D values (v scaled by mul; NTH threads) -> the fixed-point
-// exponent F with max |v| 2^F < 2^22, capped at 60.
-template <int NH, int NTH>
-__device__ __forceinline__ int fixed_exponent(const float* v, float mul, float* red, int tid) {
-    float mx = 0.0f;
-    for (int i = tid; i < NH * D; i += NTH) mx = fmaxf(mx, fabsf(v[i] * mul));
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NTH / 64; ++w) mx = fmaxf(mx, red[w]);
-    int e = 0;
-    if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
-    const int F = 22 - e;
-    return F > 60 ? 60 : F;
-}
-
-// The q-side image of group grp into out[IMG_DW].  Every thread of the block (NTH >= 512
-// threads) calls it: it holds barriers.
-template <bool QJL, int GC, int NTH>
-__device__ __forceinline__ void build_image(const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, int grp,
-                                            const float* __restrict__ Rk, const float* __restrict__ S, float c_mse,
-                                            float c_qjl, PrepLds<GC>& L, uint32_t* out, int tid) {
-    static_assert(NTH >= 512 && NTH <= 1024 && NTH % 64 == 0, "image builder threads");
+// Phase 1 (no barriers).  R_k tiles write their part of the key-score image; S tiles write
+// q_proj to L.qp and their max |q_proj| to L.red.  mid() runs in every wave after this wave's
+// operand loads are issued and before they are waited for: global loads complete in issue
+// order, so loads that mid() issues stay in flight through the products (and the barriers,
+// which wait for LDS only).
+template <bool QJL, int GC, int NW, typename Mid>
+__device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, int G, int bh0,
+                                               const float* __restrict__ Rk, const float* __restrict__ S,
+                                               float c_mse, PrepLds<GC>& L, uint32_t* img, int wave, int lane,
+                                               Mid&& mid) {
     using R = Rows<GC>;
     constexpr int NH = R::NH;
-    const int lane = tid & 63;
-    const int b = grp / kv_heads, kvh = grp - b * kv_heads;
-    const int bh0 = b * q_heads + kvh * G;
-
-    constexpr int QPT = (NH * D + NTH - 1) / NTH;  // query values per thread
-    uint32_t qv[QPT];
+    constexpr int NTILE = QJL ? 16 : 8;
+    constexpr int TPW = (NTILE + NW - 1) / NW;  // tiles per wave
+    const bool active = wave < NTILE;           // wave-uniform
+    const int c = lane & 15, kq = lane >> 4;
+    // A: lane (row c = query head, kq) holds q[c][32 s + 8 kq + e] for k-step s
+    u32x4 qa[4];
+    // B: lane (column c, kq) holds row 16 t' + c, elements 32 s + 8 kq + e
+    float4 rr[TPW][8];
+    if (active) {
+        // rows c >= G are zero: every lane loads a valid row (no branch, so no wait here) and
+        // the unused ones are cleared after the wait
+        const uint16_t* qrow = q + (size_t)(bh0 + (c < G ? c : 0)) * D + 8 * kq;
 #pragma unroll
-    for (int k = 0; k < QPT; ++k) {
-        const int i = tid + k * NTH, h = i / D, d = i % D;
-        qv[k] = (i < NH * D && h < G) ? (uint32_t)q[(size_t)(bh0 + h) * D + d] : 0u;
-    }
-    constexpr int MATS = QJL ? 2 : 1;
-    const bool mv_thread = tid < MATS * 2 * D;
-    const int hf = tid & 1, j = (tid >> 1) & (D - 1), mat = (tid >> 8) & 1;
-    float4 r4[16];
-    if (mv_thread) {
-        const float4* row = reinterpret_cast<const float4*>((mat ? S : Rk) + (size_t)j * D) + 16 * hf;
+        for (int s = 0; s < 4; ++s) qa[s] = *reinterpret_cast<const u32x4*>(qrow + 32 * s);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) r4[i] = row[i];
-    }
+        for (int u = 0; u < TPW; ++u) {
+            const int t = wave + u * NW;
+            if (t < NTILE) {
+                const float* row = (t < 8 ? Rk : S) + (size_t)(16 * (t & 7) + c) * D + 8 * kq;
 #pragma unroll
-    for (int k = 0; k < QPT; ++k) {
-        const int i = tid + k * NTH;
-        if (i < NH * D) L.qs[i / D][i % D] = tq::bf16_to_f32(qv[k]);
-    }
-    __syncthreads();
-    if (mv_thread) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            const float4* qh = reinterpret_cast<const float4*>(L.qs[h]) + 16 * hf;
-            float a = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float4 x = qh[i];
-                a = __builtin_fmaf(x.x, r4[i].x, a);
-                a = __builtin_fmaf(x.y, r4[i].y, a);
-                a = __builtin_fmaf(x.z, r4[i].z, a);
-                a = __builtin_fmaf(x.w, r4[i].w, a);
+                for (int s = 0; s < 4; ++s) {
+                    rr[u][2 * s] = *reinterpret_cast<const float4*>(row + 32 * s);
+                    rr[u][2 * s + 1] = *reinterpret_cast<const float4*>(row + 32 * s + 4);
+                }
             }
-            a += __shfl_xor(a, 1);
-            if (hf == 0) (mat ? L.qp : L.qr)[h][j] = a;
         }
     }
-    __syncthreads();
-
-    int G2 = 0;  // QJL fixed-point exponent: y_d = q_proj_d 2^G2 (to rounding)
-    if constexpr (QJL) {
-        // The split kernel feeds sign bit i = d % 8 of every byte in place (byte value 2^i, or
-        // -128 for i = 7), so dim d carries x_d = rint(q_proj_d 2^(G2 - i)) (negated for i = 7)
-        // and contributes y_d = x_d 2^i; |x_d| < 2^29 in four balanced int8 limbs.
-        G2 = fixed_exponent<NH, NTH>(&L.qp[0][0], 1.0f, L.red, tid) + 7;
-        // thread -> (head h, dim d); a wave covers 64 dims of one head, whose sum of y is
-        // exact in fp64
-        uint8_t* lb = reinterpret_cast<uint8_t*>(&L.limb[0][0][0][0]);
-        for (int i = tid; i < NH * D; i += NTH) {
-            const int h = i / D, d = i % D, bit = d & 7;
-            const int x = (int)rintf(L.qp[h][d] * ldexpf(1.0f, G2 - bit));
-            double ys = (double)x * (double)(1 << bit);
+    __builtin_amdgcn_sched_barrier(0);
+    mid();
+    __builtin_amdgcn_sched_barrier(0);
+    if (!active) return;
+    if (c >= G) {
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) ys += __shfl_xor(ys, off);
-            if (lane == 0) L.sqd[i >> 6] = ys;
-            put_limbs<NH>(lb, h, d, bit == 7 ? -x : x);
-        }
-        __syncthreads();
+        for (int s = 0; s < 4; ++s) qa[s] = u32x4{0u, 0u, 0u, 0u};
     }
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+        const int t = wave + u * NW;
+        if (t >= NTILE) break;
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            u32x4 hi, mid, lo;
+            split3_bf16(rr[u][2 * s], rr[u][2 * s + 1], hi, mid, lo);
+            acc = mfma_bf16(qa[s], lo, acc);
+            acc = mfma_bf16(qa[s], mid, acc);
+            acc = mfma_bf16(qa[s], hi, acc);
+        }
+        // lane (c, kq) holds rows 4 kq + i (query heads) of column j
+        const int j = 16 * (t & 7) + c;
+        if (t < 8) {
+            // key-score image: dword (jj, lane (n, gq), r) holds dim j = 32 gq + 4 jj + r of row n
+            if (4 * kq < NH) {
+                const int gq = j >> 5, jj = (j >> 2) & 7, r = j & 3;
+                uint32_t* base = img + IMG_QA + (jj * 64 + 16 * gq) * 4 + r;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int h = 4 * kq + i;
+                    const float x = acc[i] * c_mse;  // scores come out in log2 units
+                    const float xh = bf16_val(bf16_bits(x));
+                    base[R::row(h, 0) * 4] = dup_bf16(xh);
+                    base[R::row(h, 1) * 4] = dup_bf16(x - xh);
+                    if constexpr (GC == 1) {  // rows 4 h + 2, 4 h + 3 are unused
+                        base[R::row(h, 2) * 4] = 0u;
+                        base[R::row(h, 3) * 4] = 0u;
+                    }
+                }
+            }
+        } else {
+            if (4 * kq < NH) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) L.qp[4 * kq + i][j] = acc[i];
+            }
+            float mx = fmaxf(fmaxf(fabsf(acc[0]), fabsf(acc[1])), fmaxf(fabsf(acc[2]), fabsf(acc[3])));
+            mx = row_max16(mx);  // then the four rows of 16 lanes
+            mx = fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0)),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16))),
+                       fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48))));
+            if (lane == 0) L.red[t - 8] = mx;
+        }
+    }
+}
 
-    // key-score A operand image: dword (j, lane, r)
-    for (int i = tid; i < 8 * 64 * 4; i += NTH) {
-        const int jj = i >> 8, ln = (i >> 2) & 63, r = i & 3;
-        const int n = ln & 15, g = ln >> 4;
-        const int h_row = GC == 1 ? n / 4 : n / 2;
-        const int x_row = GC == 1 ? n % 4 : n % 2;
-        uint32_t v = 0;
-        if (x_row < 2 && h_row < G) {
-            const float x = L.qr[h_row][32 * g + 4 * jj + r] * c_mse;  // scores come out in log2 units
-            const float hi = bf16_val(bf16_bits(x));
-            v = dup_bf16(x_row == 0 ? hi : x - hi);
+// Phase 2 (after a barrier): the QJL fixed-point exponent G2 (max |q_proj| 2^(G2 - 7) < 2^22,
+// G2 - 7 capped at 60) and the limb image.  Returns G2 in every thread.
+template <int GC, int NT>
+__device__ __forceinline__ int qjl_image(const PrepLds<GC>& L, uint32_t* img, int tid) {
+    constexpr int NH = 4 * GC;
+    float mx = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) mx = fmaxf(mx, L.red[w]);
+    int e = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
+    int F = 22 - e;
+    F = F > 60 ? 60 : F;
+    const int G2 = F + 7;
+    uint8_t* ib = reinterpret_cast<uint8_t*>(img + IMG_QJ);
+    for (int i = tid; i < NH * D; i += NT) {
+        const int h = i / D, d = i % D, bit = d & 7;
+        int x = (int)rintf(L.qp[h][d] * ldexpf(1.0f, G2 - bit));
+        if (bit == 7) x = -x;  // bit 7 of a sign byte is worth -128
+        const int gq = d >> 5, jj = bit >> 2, v = bit & 3, e8 = (d >> 3) & 3;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int l = ((x + 128) & 255) - 128;  // balanced base-256 digit k
+            const int set = GC == 1 ? 0 : k >> 1;
+            const int n = GC == 1 ? 4 * h + k : 2 * h + (k & 1);
+            ib[(((set * 2 + jj) * 64 + 16 * gq + n) * 4 + v) * 4 + e8] = (uint8_t)(l & 255);
+            x = (x - l) >> 8;
         }
-        out[IMG_QA + i] = v;
     }
-    if constexpr (QJL) {
-        for (int i = tid; i < R::NQJ * 2 * 64 * 4; i += NTH) {
-            const int set = i >> 9, jj = (i >> 8) & 1, ln = (i >> 2) & 63, v = i & 3;
-            const int n = ln & 15, g = ln >> 4;
-            const int h = GC == 1 ? n / 4 : n / 2;
-            const int l = GC == 1 ? n % 4 : 2 * set + (n % 2);
-            out[IMG_QJ + i] = L.limb[l][h][g][4 * jj + v];
-        }
-        if (tid < NH) {
-            const float sqv =
-                (float)((L.sqd[2 * tid] + L.sqd[2 * tid + 1]) * (double)ldexpf(1.0f, -G2) * (double)c_qjl);
-            out[IMG_SQ + tid] = __float_as_uint(sqv);
-        }
-        if (tid == 0) out[IMG_QFIX] = __float_as_uint(ldexpf(1.0f, 1 - G2) * c_qjl);
+    return G2;
+}
+
+// sum_d y_d s_d of the lane's head i from the QJL MFMA accumulators (four limb sums, each
+// |.| <= 2^21): pairs exact in int32, then one fp32 rounding
+template <int GC>
+__device__ __forceinline__ float qjl_combine(const i32x4 (&acc)[GC], int i) {
+    int lo, hi;
+    if constexpr (GC == 1) {
+        lo = acc[0][0] + (acc[0][1] << 8);
+        hi = acc[0][2] + (acc[0][3] << 8);
+    } else {
+        lo = acc[0][2 * i] + (acc[0][2 * i + 1] << 8);
+        hi = acc[1][2 * i] + (acc[1][2 * i + 1] << 8);
     }
+    return __builtin_fmaf((float)hi, 65536.0f, (float)lo);
 }
 
 
@@ -529,7 +553,6 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     using R = Rows<GC>;
     constexpr int NW = Cfg<VB, GC, QJL>::NW;
     constexpr int NT = Cfg<VB, GC, QJL>::NT;
-    constexpr int NH = R::NH;
     constexpr int KROW = D * KB / 8;  // bytes per key row
     constexpr int VROW = D * VB / 8;  // bytes per value row
     constexpr int VCH = 8 * VB;       // bits of one lane's 8-dim value chunk
@@ -657,37 +680,54 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 
     // ------------------------------------------------------------ prologue
     // phase 1: codebooks (hi|lo) and the group's q-side image (every split workgroup of the
-    // group computes it: two 128 x 128 mat-vecs per head from L2-resident R_k and S, cheaper
+    // group computes it: the mat-vecs on the matrix cores from L2-resident R_k and S, cheaper
     // than a separate launch ahead of the split pass)
-    if (tid < (1 << KB)) sm.u.pro.ksrc[tid] = pack_hilo(Ck[tid]);
-    if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = pack_hilo(Cv[tid - 64]);
-    build_image<QJL, GC, NT>(q, q_heads, kv_heads, G, grp, Rk, S, c_mse, c_qjl, sm.u.pro.ps,
-                             reinterpret_cast<uint32_t*>(sm.u.pro.img), tid);
+    uint32_t* img = reinterpret_cast<uint32_t*>(sm.u.pro.img);
+    // every global load of the prologue is issued before any is waited for: the codebook entries
+    // (unconditionally, in range), the products' operands, then the first blocks of the token
+    // loop, whose HBM latency the rest of the prologue covers
+    const float ck_e = Ck[tid & ((1 << KB) - 1)];
+    const float cv_e = Cv[tid & ((1 << VB) - 1)];
+    image_products<QJL, GC, NW>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, wave, lane, [&] {
+#pragma unroll
+        for (int s = 0; s < NSET; ++s) {
+            load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    });
+    if (tid < (1 << KB)) sm.u.pro.ksrc[tid] = pack_hilo(ck_e);
+    if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = pack_hilo(cv_e);
     // zero slots of the weight transpose (never written by the loop)
     for (int i = tid; i < NW * 16 * Sm::WTS; i += NT) (&sm.wt[0][0][0])[i] = 0u;
     __syncthreads();
-    // phase 2 (LDS only): pair tables expanded from the codebooks; operands into registers
-    for (int i = tid; i < (1 << (2 * KB)) * Sm::KC; i += NT) {
-        const int e = i / Sm::KC;
-        (&sm.ktab[0][0])[i] = make_uint2(sm.u.pro.ksrc[e & ((1 << KB) - 1)], sm.u.pro.ksrc[e >> KB]);
+    // phase 2 (LDS only): the QJL limb image; pair tables expanded from the codebooks, two
+    // neighbouring copies of an entry per 16-byte write
+    int G2 = 0;
+    if constexpr (QJL) G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid);
+    for (int i = tid; i < (1 << (2 * KB)) * Sm::KC / 2; i += NT) {
+        const int e = i / (Sm::KC / 2);
+        const uint32_t lo = sm.u.pro.ksrc[e & ((1 << KB) - 1)], hi = sm.u.pro.ksrc[e >> KB];
+        reinterpret_cast<uint4*>(&sm.ktab[0][0])[i] = make_uint4(lo, hi, lo, hi);
     }
     if constexpr (Sm::PT) {
-        for (int i = tid; i < (1 << (2 * VB)) * VCOPIES; i += NT) {
-            const int e = i / VCOPIES;
-            (&sm.vtab2[0][0])[i] = make_uint2(sm.vtab[e & ((1 << VB) - 1)], sm.vtab[e >> VB]);
+        for (int i = tid; i < (1 << (2 * VB)) * VCOPIES / 2; i += NT) {
+            const int e = i / (VCOPIES / 2);
+            const uint32_t lo = sm.vtab[e & ((1 << VB) - 1)], hi = sm.vtab[e >> VB];
+            reinterpret_cast<uint4*>(&sm.vtab2[0][0])[i] = make_uint4(lo, hi, lo, hi);
         }
     }
-    const uint32_t* im = reinterpret_cast<const uint32_t*>(sm.u.pro.img);
-    // A operands of the key-score MFMAs (32 VGPRs): lane (n, g), MFMA j, VGPR r holds
-    // q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo codebook parts).
+    __syncthreads();
+    // phase 3: operands into registers.  A operands of the key-score MFMAs (32 VGPRs): lane
+    // (n, g), MFMA j, VGPR r holds q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo
+    // codebook parts).
     u32x4 qa[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qa[j] = *reinterpret_cast<const u32x4*>(im + IMG_QA + (j * 64 + lane) * 4);
+    for (int j = 0; j < 8; ++j) qa[j] = *reinterpret_cast<const u32x4*>(img + IMG_QA + (j * 64 + lane) * 4);
     // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
     // 32 g + 4 jj + v + 8 e.
     u32x4 qj[R::NQJ][2];
     float sq[R::HPL];
-    float qfix = 0.0f;  // sum_d qp s_d = 2 (sum_{bit=1} qp) - sum qp, in units of 2^-F
+    float qfix = 0.0f;  // QJL logit per unit of sum_{s_d = 1} y_d (y_d = q_proj_d 2^G2 to rounding)
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) sq[i] = 0.0f;
     if constexpr (QJL) {
@@ -695,12 +735,24 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         for (int set = 0; set < R::NQJ; ++set)
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
-                qj[set][jj] = *reinterpret_cast<const u32x4*>(im + IMG_QJ + ((set * 2 + jj) * 64 + lane) * 4);
+                qj[set][jj] = *reinterpret_cast<const u32x4*>(img + IMG_QJ + ((set * 2 + jj) * 64 + lane) * 4);
+        // sum_d q_proj s_d = 2 sum_{s_d = 1} q_proj - sum_d q_proj; sum_d y_d is the QJL MFMA
+        // against a token whose sign bits are all set (the same arithmetic as every token's sum)
+        qfix = ldexpf(1.0f, 1 - G2) * c_qjl;
+        u32x4 ones[2];
 #pragma unroll
-        for (int i = 0; i < R::HPL; ++i) sq[i] = __uint_as_float(im[IMG_SQ + R::HPL * g + i]);
-        qfix = __uint_as_float(im[IMG_QFIX]);
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) ones[jj][v] = 0x01010101u << (4 * jj + v);
+        i32x4 acc_all[R::NQJ];
+#pragma unroll
+        for (int set = 0; set < R::NQJ; ++set) {
+            acc_all[set] = mfma_i8(qj[set][0], ones[0], i32x4{0, 0, 0, 0});
+            acc_all[set] = mfma_i8(qj[set][1], ones[1], acc_all[set]);
+        }
+#pragma unroll
+        for (int i = 0; i < R::HPL; ++i) sq[i] = qjl_combine<GC>(acc_all, i) * (0.5f * qfix);
     }
-    __syncthreads();  // the prologue area is reused by the epilogue
 
     // per-lane softmax state (heads of this lane group) and value accumulators
     float m_ref[R::HPL], s_lane[R::HPL];
@@ -786,16 +838,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             const float ksum = (acc_k[2 * i] + acc_k1[2 * i]) + (acc_k[2 * i + 1] + acc_k1[2 * i + 1]);
             float v;
             if constexpr (QJL) {
-                // sum_d y_d s_d from the four limb sums (each |.| <= 2^21): pairs exact in int32
-                int lo, hi;
-                if constexpr (GC == 1) {
-                    lo = acc_q[0][0] + (acc_q[0][1] << 8);
-                    hi = acc_q[0][2] + (acc_q[0][3] << 8);
-                } else {
-                    lo = acc_q[0][2 * i] + (acc_q[0][2 * i + 1] << 8);
-                    hi = acc_q[1][2 * i] + (acc_q[1][2 * i + 1] << 8);
-                }
-                const float qi = __builtin_fmaf((float)hi, 65536.0f, (float)lo);
+                const float qi = qjl_combine<GC>(acc_q, i);  // sum_d y_d s_d
                 v = __builtin_fmaf(knf, ksum, __builtin_fmaf(krf, __builtin_fmaf(qi, qfix, -sq[i]), 0.0f));
             } else {
                 v = knf * ksum;
@@ -976,11 +1019,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         __builtin_amdgcn_s_setprio(0);
     };
 
-#pragma unroll
-    for (int s = 0; s < NSET; ++s) {
-        load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    // (the first NSET blocks were issued in the prologue)
     if (nb > 0) {
         auto process = [&](const Kd& K_, const Vd& V_, int rel) {
             float lg[R::HPL];
@@ -1005,6 +1044,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     }
 
     // ------------------------------------------------------------ epilogue
+    __syncthreads();  // the prologue area (read by every wave's phase 3) is reused below
     float s_row[R::HPL];
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) s_row[i] = row_sum16(s_lane[i]);
@@ -1502,8 +1542,9 @@ int decode_attention_impl(const uint16_t* q, int batch, int q_heads, int kv_head
     if (!out_f32 && !out_bf16 && !lse_out) return TQ_ERR_INVALID_ARGUMENT;
     if (n_tokens > 0 && (!k_codes || !k_norms || !v_codes || !v_norms)) return TQ_ERR_INVALID_ARGUMENT;
     if (has_qjl && (!qjl || (n_tokens > 0 && (!k_signs || !k_rnorms)))) return TQ_ERR_INVALID_ARGUMENT;
-    if ((k_codes && !aligned16(k_codes)) || (k_signs && !aligned16(k_signs)) || (v_codes && !aligned16(v_codes)) ||
-        !aligned16(key_rotation) || !aligned16(value_rotation) || (qjl && !aligned16(qjl)))
+    if (!aligned16(q) || (k_codes && !aligned16(k_codes)) || (k_signs && !aligned16(k_signs)) ||
+        (v_codes && !aligned16(v_codes)) || !aligned16(key_rotation) || !aligned16(value_rotation) ||
+        (qjl && !aligned16(qjl)))
         return TQ_ERR_UNSUPPORTED;
     const bool combo_ok = has_qjl ? (key_bits + 1 == value_bits && value_bits >= 2 && value_bits <= 4)
                                   : (key_bits == value_bits && key_bits >= 1 && key_bits <= 4);

@@ -88,9 +88,6 @@ struct SChunk {
     sf16 a[CH / 16];
     __device__ __forceinline__ float operator[](int k) const { return a[k >> 4][k & 15]; }
 };
-__device__ __forceinline__ void sload(SChunk<16>& c, const float* p) {
-    asm volatile("s_load_dwordx16 %0, %1, 0x0" : "=&s"(c.a[0]) : "s"(p) : "memory");
-}
 __device__ __forceinline__ void sload(SChunk<32>& c, const float* p) {
     asm volatile("s_load_dwordx16 %0, %2, 0x0\n\ts_load_dwordx16 %1, %2, 0x40"
                  : "=&s"(c.a[0]), "=&s"(c.a[1])
@@ -98,7 +95,6 @@ __device__ __forceinline__ void sload(SChunk<32>& c, const float* p) {
                  : "memory");
 }
 // completes every outstanding scalar load (and LDS access); c is valid afterwards
-__device__ __forceinline__ void swait(SChunk<16>& c) { asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c.a[0])); }
 __device__ __forceinline__ void swait(SChunk<32>& c) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c.a[0]), "+s"(c.a[1]));
 }
