@@ -177,6 +177,12 @@ __device__ __forceinline__ uint32_t and_byte(uint32_t w, uint32_t mask) {
     }
 }
 
+// Bits [sh, sh + 32) of the 64-bit pair hi:lo, sh in [0, 64): one v_lshrrev_b64 whatever the
+// lane's shift (a select between an alignbit and a 32-bit shift became a lane-divergent branch)
+__device__ __forceinline__ uint32_t shr64(uint32_t lo, uint32_t hi, int sh) {
+    return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
     const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : (int)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, BUF_DW3);
@@ -918,7 +924,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             uint32_t ch[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                ch[r] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh) : B.vw[r][1] >> (vsh - 32);
+                ch[r] = shr64(B.vw[r][0], B.vw[r][1], vsh);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
 #pragma unroll
@@ -954,7 +960,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if constexpr (VB == 3)
-                    ch[r] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh) : B.vw[r][1] >> (vsh - 32);
+                    ch[r] = shr64(B.vw[r][0], B.vw[r][1], vsh);
                 else
                     ch[r] = B.vw[r][0];
             }
@@ -981,8 +987,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if constexpr (VB == 3)
-                    vch[r][0] = vsh < 32 ? __builtin_amdgcn_alignbit(B.vw[r][1], B.vw[r][0], vsh)
-                                         : B.vw[r][1] >> (vsh - 32);
+                    vch[r][0] = shr64(B.vw[r][0], B.vw[r][1], vsh);
                 else
                     vch[r][0] = B.vw[r][0] >> vsh;
                 if constexpr (VB == 4) {
