@@ -50,8 +50,7 @@ namespace {
 constexpr int D = TQ_DIM;
 // waves per split workgroup (one workgroup per CU), the most each kernel's registers allow
 // without spills in its loop: with at most 4 query heads per KV head, 4 per SIMD (<= 128
-// VGPRs) except 3 per SIMD for 3-bit Q_prod values; with 5..8 heads, 3 per SIMD (<= 168)
-// except 2 per SIMD for 3-bit values
+// VGPRs); with 5..8 heads, 3 per SIMD (<= 168)
 #ifndef TQ_ATTN_WAVES_G4
 #define TQ_ATTN_WAVES_G4 16
 #endif
@@ -66,7 +65,7 @@ constexpr int D = TQ_DIM;
 #endif
 template <int VB, int GC, bool QJL>
 struct Cfg {
-    static constexpr int NW = GC == 1 ? ((VB == 3 && QJL) ? 12 : TQ_ATTN_WAVES_G4) : (VB == 3 ? 8 : TQ_ATTN_WAVES_G8);
+    static constexpr int NW = GC == 1 ? TQ_ATTN_WAVES_G4 : TQ_ATTN_WAVES_G8;
     static constexpr int NT = NW * 64;
     // per-wave blocks in flight (register sets of packed data)
     static constexpr int NSET = GC == 1 ? TQ_ATTN_SETS_G4 : TQ_ATTN_SETS_G8;
@@ -177,10 +176,13 @@ __device__ __forceinline__ uint32_t and_byte(uint32_t w, uint32_t mask) {
     }
 }
 
-// Bits [sh, sh + 32) of the 64-bit pair hi:lo, sh in [0, 64): one v_lshrrev_b64 whatever the
-// lane's shift (a select between an alignbit and a 32-bit shift became a lane-divergent branch)
-__device__ __forceinline__ uint32_t shr64(uint32_t lo, uint32_t hi, int sh) {
-    return (uint32_t)((((uint64_t)hi << 32) | lo) >> sh);
+// A lane's 24-bit chunk of 3-bit value codes at bit sh of its dword w (sh in {0, 8, 16, 24}),
+// aligned to bit 0: the bits past w come from the next lane of the row of 16 (DPP row_shl:1,
+// lane i reads lane i + 1), whose dword is the following one of the code row wherever the chunk
+// straddles.  Bits 24..31 of the result are not part of the chunk.
+__device__ __forceinline__ uint32_t chunk3(uint32_t w, int sh) {
+    const uint32_t next = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w, 0x101, 0xF, 0xF, false);
+    return __builtin_amdgcn_alignbit(next, w, sh);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
@@ -272,6 +274,7 @@ struct Smem {
     union {
         struct {
             uint4 img[IMG_DW / 4];      // this group's q-side image
+            uint4 qst[NW][NH * 16];     // per-wave copy of the group's query rows
             uint32_t ksrc[16];          // Ck hi|lo per key code
             PrepLds<GC> ps;             // scratch of the image builder
         } pro;
@@ -411,8 +414,8 @@ __device__ __forceinline__ void split3_bf16(const float4& a, const float4& b, u3
 template <bool QJL, int GC, int NW, typename Mid>
 __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, int G, int bh0,
                                                const float* __restrict__ Rk, const float* __restrict__ S,
-                                               float c_mse, PrepLds<GC>& L, uint32_t* img, int wave, int lane,
-                                               Mid&& mid) {
+                                               float c_mse, PrepLds<GC>& L, uint32_t* img, uint4* qst,
+                                               int wave, int lane, Mid&& mid) {
     using R = Rows<GC>;
     constexpr int NH = R::NH;
     constexpr int NTILE = QJL ? 16 : 8;
@@ -423,12 +426,14 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
     u32x4 qa[4];
     // B: lane (column c, kq) holds row 16 t' + c, elements 32 s + 8 kq + e
     float4 rr[TPW][8];
+    // the group's query rows, 16 bytes per lane (rows >= G read as zero through the descriptor),
+    // restaged in the wave's LDS slot below: one load per NH / 4 rows instead of four per lane,
+    // most of them repeats of the same rows
+    u32x4 qv[NH / 4];
     if (active) {
-        // rows c >= G are zero: every lane loads a valid row (no branch, so no wait here) and
-        // the unused ones are cleared after the wait
-        const uint16_t* qrow = q + (size_t)(bh0 + (c < G ? c : 0)) * D + 8 * kq;
+        const __amdgpu_buffer_rsrc_t rq = rsrc(q + (size_t)bh0 * D, (int64_t)G * D * 2);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) qa[s] = *reinterpret_cast<const u32x4*>(qrow + 32 * s);
+        for (int i = 0; i < NH / 4; ++i) qv[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, (i * 64 + lane) * 16, 0, 0);
 #pragma unroll
         for (int u = 0; u < TPW; ++u) {
             const int t = wave + u * NW;
@@ -446,6 +451,14 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
     mid();
     __builtin_amdgcn_sched_barrier(0);
     if (!active) return;
+    // the wave's own LDS slot: its accesses execute in order, no barrier needed
+#pragma unroll
+    for (int i = 0; i < NH / 4; ++i) qst[i * 64 + lane] = __builtin_bit_cast(uint4, qv[i]);
+    {
+        const int cr = c < NH ? c : 0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qa[s] = __builtin_bit_cast(u32x4, qst[cr * 16 + 4 * s + kq]);
+    }
     if (c >= G) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) qa[s] = u32x4{0u, 0u, 0u, 0u};
@@ -614,10 +627,14 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     const int so = n * (D / 8) + 4 * g;          // sign bits of token n, same dims
     const int no = 2 * n;                        // f16 norms of token n
     const int vbit0 = VCH * n;                   // value chunk of lane n: dims [8 n, 8 n + 8)
-    // first dword read for the chunk; 3-bit chunks read two dwords, kept inside the row
-    const int vdw = VB == 3 ? ((vbit0 >> 5) < VROW / 4 - 2 ? (vbit0 >> 5) : VROW / 4 - 2) : (vbit0 >> 5);
+    // the dword holding the chunk's first bit, and the chunk's offset in it.  A 3-bit chunk (24
+    // bits at 24 n) straddles two dwords only for n = 1, 2 mod 4 (offsets 24, 16), and then its
+    // second dword is the first dword of lane n + 1's chunk: each lane reads one dword per row
+    // and takes the next one from its neighbour (reading both dwords in every lane made the
+    // value stream ~16% slower to load)
+    const int vdw = vbit0 >> 5;
     const int vo = 4 * vdw + g * VROW;           // + 4 r VROW for token 4 r + g (each load: 4 whole rows)
-    const int vsh = vbit0 - 32 * vdw;            // in [0, 64) for VB == 3, [0, 32) otherwise
+    const int vsh = vbit0 - 32 * vdw;            // in [0, 32)
 
     // Per-block data of a wave, in the part the score stage reads (key codes, sign bits and
     // the three norms of token n) and the part the value stage reads (value codes of tokens
@@ -628,7 +645,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         uint32_t kn, kr, vn;  // norms (f16 bits) of token n
     };
     struct Vd {
-        uint32_t vw[4][2];    // value codes of tokens 4 r + g, lane n's dword(s)
+        uint32_t vw[4];       // value codes of tokens 4 r + g, the dword holding lane n's chunk start
     };
     auto load_k = [&](Kd& B, int rel_) {
         const int rel = __builtin_amdgcn_readfirstlane(rel_);  // scalar block offset
@@ -658,14 +675,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         const int rel = __builtin_amdgcn_readfirstlane(rel_);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            if constexpr (VB == 3) {
-                // the 24-bit chunk may straddle two dwords: read the (in-row) pair holding it
-                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + 4 * r * VROW, rel * VROW, KV_NT);
-                B.vw[r][0] = w.x, B.vw[r][1] = w.y;
-            } else {
-                B.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + 4 * r * VROW, rel * VROW, KV_NT);
-                B.vw[r][1] = 0u;
-            }
+            B.vw[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + 4 * r * VROW, rel * VROW, KV_NT);
         }
     };
 
@@ -694,7 +704,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // loop, whose HBM latency the rest of the prologue covers
     const float ck_e = Ck[tid & ((1 << KB) - 1)];
     const float cv_e = Cv[tid & ((1 << VB) - 1)];
-    image_products<QJL, GC, NW>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, wave, lane, [&] {
+    image_products<QJL, GC, NW>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, sm.u.pro.qst[wave], wave, lane, [&] {
 #pragma unroll
         for (int s = 0; s < NSET; ++s) {
             load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
@@ -924,7 +934,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             uint32_t ch[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                ch[r] = shr64(B.vw[r][0], B.vw[r][1], vsh);
+                ch[r] = chunk3(B.vw[r], vsh);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
 #pragma unroll
@@ -946,8 +956,8 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                     // LDS byte offset 256 * byte m + plane in one v_perm: [plane, byte m, 0, 0]
                     constexpr uint32_t SEL_LO = 0x0C0C0000u;
                     const uint32_t sel = SEL_LO | ((4u + (uint32_t)m) << 8);
-                    const uint32_t o0 = __builtin_amdgcn_perm(B.vw[2 * u][0], plane, sel);
-                    const uint32_t o1 = __builtin_amdgcn_perm(B.vw[2 * u + 1][0], plane, sel);
+                    const uint32_t o0 = __builtin_amdgcn_perm(B.vw[2 * u], plane, sel);
+                    const uint32_t o1 = __builtin_amdgcn_perm(B.vw[2 * u + 1], plane, sel);
                     const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
                     const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
                     acc_v[m] = mfma_bf16(av.a[u], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
@@ -960,9 +970,9 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if constexpr (VB == 3)
-                    ch[r] = shr64(B.vw[r][0], B.vw[r][1], vsh);
+                    ch[r] = chunk3(B.vw[r], vsh);
                 else
-                    ch[r] = B.vw[r][0];
+                    ch[r] = B.vw[r];
             }
 #pragma unroll
             for (int pb = 0; pb < 4; ++pb) {
@@ -987,9 +997,9 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if constexpr (VB == 3)
-                    vch[r][0] = shr64(B.vw[r][0], B.vw[r][1], vsh);
+                    vch[r][0] = chunk3(B.vw[r], vsh);
                 else
-                    vch[r][0] = B.vw[r][0] >> vsh;
+                    vch[r][0] = B.vw[r] >> vsh;
                 if constexpr (VB == 4) {
                     vch[r][1] = vch[r][0] >> 2;
                     vch[r][0] = vch[r][0] << 2;
