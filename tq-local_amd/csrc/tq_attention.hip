@@ -1043,14 +1043,15 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             weights(lg, K_.vn, av);
             values(V_, av);
         };
-        // whole rounds of NSET blocks, also without a branch around each block: up to NSET - 1
-        // blocks past the range are processed (all their tokens are masked, weights 0; the
-        // wave's first block was in range, so the reference maximum is finite by then)
+        // whole rounds of NSET blocks: up to NSET - 1 blocks past the range end the wave's last
+        // round, and a wave-uniform branch skips their processing (not their refill loads, which
+        // stay unconditional).  Skipping matters where a workgroup's blocks do not divide
+        // evenly among its waves (C4: 128 blocks over 12 waves, -0.8 us per call; C5 shape -1.4)
         for (int i = 0; i < nb; i += NSET) {
 #pragma unroll
             for (int s = 0; s < NSET; ++s) {
                 const int rel = first + (i + s) * STEP;
-                process(kset[s], vset[s], rel);
+                if (rel < nt) process(kset[s], vset[s], rel);
                 __builtin_amdgcn_sched_barrier(0);
                 load_k(kset[s], rel + NSET * STEP), load_v(vset[s], rel + NSET * STEP);
                 __builtin_amdgcn_sched_barrier(0);
