@@ -85,6 +85,8 @@ CASES = [
     (1, 6, 2, 100, 1, False),     # GQA 3, 1-bit
     (3, 12, 2, 333, 4, False),    # GQA 6, 4-bit Q_mse
     (1, 2, 2, 1, 4, True),        # a single token
+    (1, 8, 2, 777, 2, True),      # 2-bit Q_prod (1-bit MSE keys + QJL, 2-bit values)
+    (2, 12, 2, 450, 3, False),    # GQA 6, 3-bit Q_mse (3-bit value pairs across lanes)
 ]
 
 
