@@ -225,10 +225,8 @@ def dequantize_prod(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Tenso
     return out
 
 
-#: partials workspace per (device, stream): calls on one stream are ordered, so they can
-#: share one; calls on two streams get two
-#: partials workspace per (device, stream): calls on one stream are ordered, so they can
-#: share one; calls on two streams get two
+#: attention workspace (call counter, partials, shared q-side tiles) per (device, stream):
+#: calls on one stream are ordered, so they can share one; calls on two streams get two
 _workspaces: dict[tuple, torch.Tensor] = {}
 #: workspaces replaced by a larger one stay allocated: a HIP graph that captured a call keeps
 #: the old pointer and may be replayed later
