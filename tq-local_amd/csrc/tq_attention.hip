@@ -963,6 +963,29 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                     acc_v[m] = mfma_bf16(av.a[u], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
                 }
             }
+        } else if constexpr (PAIR_COLS<VB, GC> && VB == 4) {
+            // generic layout, 4-bit: one pair-table lookup per two tokens of one dim.  Lane (n, g)
+            // supplies tokens 4 r + g (k-slots 8 g + 2 r + y); byte b of tp[k][par] holds the codes
+            // of dim 8 n + 2 b + par of tokens 4 (2 k) + g (low nibble) and 4 (2 k + 1) + g (high
+            // nibble), so a lookup returns the (Cv hi|lo) dwords of two consecutive k-slot pairs of
+            // one MFMA operand, in register order
+            uint32_t tp[2][2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t a = B.vw[2 * k], b = B.vw[2 * k + 1];
+                tp[k][0] = (a & 0x0F0F0F0Fu) | ((b << 4) & 0xF0F0F0F0u);
+                tp[k][1] = ((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u);
+            }
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                // LDS byte offset 256 * byte (m / 2) + plane in one v_perm: [plane, byte, 0, 0]
+                const uint32_t sel = 0x0C0C0000u | ((4u + (uint32_t)(m >> 1)) << 8);
+                const uint32_t o0 = __builtin_amdgcn_perm(tp[0][m & 1], plane, sel);
+                const uint32_t o1 = __builtin_amdgcn_perm(tp[1][m & 1], plane, sel);
+                const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
+                const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
+                acc_v[m] = mfma_bf16(av.a[0], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
+            }
         } else if constexpr (PAIR_COLS<VB, GC>) {
             // generic layout, one pair-table lookup per two codes: lane (n, g) supplies tokens
             // 4 r + g (k-slots 8 g + 2 r + y); pair b of its 8-dim chunk feeds MFMAs 2 b and 2 b + 1
