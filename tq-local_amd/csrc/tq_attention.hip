@@ -305,6 +305,20 @@ __device__ __forceinline__ void merge_head(int bh, int t, int n_split, const flo
 #pragma unroll
     for (int i = 0; i < 16; ++i) rvs[i] = rv4[(size_t)(16 * kr + i) * (D / 4) + c4];
     const float* ml = part_ml + (size_t)bh * n_split * 2;
+    // normalised rotated output: threads (half, d) split the splits in two.  The partials of
+    // this thread's first PF splits are loaded with the maxima, before the maximum is known, so
+    // the merge waits for one round of loads instead of two
+    const int d = t & (D - 1), hf = t >> 7;
+    constexpr int PF = 8;
+    float pv[PF], pm[PF], ps[PF];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+        const int k = hf + 2 * j;
+        const bool in = k < n_split;
+        pv[j] = in ? part_o[((size_t)bh * n_split + k) * D + d] : 0.0f;
+        pm[j] = in ? ml[2 * k] : NEG_INF;
+        ps[j] = in ? ml[2 * k + 1] : 0.0f;
+    }
     float M = NEG_INF;
     for (int k = t; k < n_split; k += MT) M = fmaxf(M, ml[2 * k]);
 #pragma unroll
@@ -312,14 +326,18 @@ __device__ __forceinline__ void merge_head(int bh, int t, int n_split, const flo
     if (lane == 0) red[wv][0] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
-    // normalised rotated output: threads (half, d) split the splits in two
-    const int d = t & (D - 1), hf = t >> 7;
     float o = 0.0f, sacc = 0.0f;
     if (M != NEG_INF) {
-        // unrolled so that several splits' loads are in flight together (the fma order is
-        // unchanged)
+        // splits hf, hf + 2, ... in order
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const float e = pm[j] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(pm[j] - M);
+            o = __builtin_fmaf(e, pv[j], o);
+            sacc = __builtin_fmaf(e, ps[j], sacc);
+        }
+        // the rest, unrolled so that several splits' loads are in flight together
 #pragma unroll 4
-        for (int k = hf; k < n_split; k += 2) {
+        for (int k = hf + 2 * PF; k < n_split; k += 2) {
             const float mk = ml[2 * k];
             const float e = mk == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
             o = __builtin_fmaf(e, part_o[((size_t)bh * n_split + k) * D + d], o);
