@@ -275,7 +275,6 @@ struct Smem {
         struct {
             uint4 img[IMG_DW / 4];      // this group's q-side image
             uint4 qst[NW][NH * 16];     // per-wave copy of the group's query rows
-            uint32_t ksrc[16];          // Ck hi|lo per key code
             PrepLds<GC> ps;             // scratch of the image builder
         } pro;
         struct {
@@ -729,28 +728,39 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             __builtin_amdgcn_sched_barrier(0);
         }
     });
-    if (tid < (1 << KB)) sm.u.pro.ksrc[tid] = pack_hilo(ck_e);
-    if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = pack_hilo(cv_e);
+    // lane l holds the hi|lo codebook entries Ck[l mod 2^KB] and Cv[l mod 2^VB]
+    const uint32_t ckp = pack_hilo(ck_e), cvp = pack_hilo(cv_e);
+    if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = cvp;
+    // pair tables from the codebooks in the lanes (ds_bpermute), two neighbouring copies of an
+    // entry per 16-byte write, by the older half of the waves: they finish their products first
+    // and wait at the barrier below for the younger ones anyway.  Every loop runs a multiple of
+    // 64 iterations per stride, so whole waves take part in each permute.
+    if (wave < NW / 2) {
+        const auto from_lane = [](uint32_t v, int l) {
+            return (uint32_t)__builtin_amdgcn_ds_bpermute(l << 2, (int)v);
+        };
+        for (int i = tid; i < (1 << (2 * KB)) * Sm::KC / 2; i += NT / 2) {
+            const int e = i / (Sm::KC / 2);
+            const uint32_t lo = from_lane(ckp, e & ((1 << KB) - 1)), hi = from_lane(ckp, e >> KB);
+            reinterpret_cast<uint4*>(&sm.ktab[0][0])[i] = make_uint4(lo, hi, lo, hi);
+        }
+        if constexpr (Sm::PT) {
+            for (int i = tid; i < (1 << (2 * VB)) * VCOPIES / 2; i += NT / 2) {
+                const int e = i / (VCOPIES / 2);
+                const uint32_t lo = from_lane(cvp, e & ((1 << VB) - 1)), hi = from_lane(cvp, e >> VB);
+                reinterpret_cast<uint4*>(&sm.vtab2[0][0])[i] = make_uint4(lo, hi, lo, hi);
+            }
+        }
+    }
     // zero slots of the weight transpose (never written by the loop)
     for (int i = tid; i < NW * 16 * Sm::WTS; i += NT) (&sm.wt[0][0][0])[i] = 0u;
     __syncthreads();
-    // phase 2 (LDS only): the QJL limb image; pair tables expanded from the codebooks, two
-    // neighbouring copies of an entry per 16-byte write
+    // phase 2 (LDS only): the QJL limb image
     int G2 = 0;
-    if constexpr (QJL) G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid);
-    for (int i = tid; i < (1 << (2 * KB)) * Sm::KC / 2; i += NT) {
-        const int e = i / (Sm::KC / 2);
-        const uint32_t lo = sm.u.pro.ksrc[e & ((1 << KB) - 1)], hi = sm.u.pro.ksrc[e >> KB];
-        reinterpret_cast<uint4*>(&sm.ktab[0][0])[i] = make_uint4(lo, hi, lo, hi);
+    if constexpr (QJL) {
+        G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid);
+        __syncthreads();
     }
-    if constexpr (Sm::PT) {
-        for (int i = tid; i < (1 << (2 * VB)) * VCOPIES / 2; i += NT) {
-            const int e = i / (VCOPIES / 2);
-            const uint32_t lo = sm.vtab[e & ((1 << VB) - 1)], hi = sm.vtab[e >> VB];
-            reinterpret_cast<uint4*>(&sm.vtab2[0][0])[i] = make_uint4(lo, hi, lo, hi);
-        }
-    }
-    __syncthreads();
     // phase 3: operands into registers.  A operands of the key-score MFMAs (32 VGPRs): lane
     // (n, g), MFMA j, VGPR r holds q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo
     // codebook parts).
