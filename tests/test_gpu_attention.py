@@ -87,6 +87,8 @@ CASES = [
     (1, 2, 2, 1, 4, True),        # a single token
     (1, 8, 2, 777, 2, True),      # 2-bit Q_prod (1-bit MSE keys + QJL, 2-bit values)
     (2, 12, 2, 450, 3, False),    # GQA 6, 3-bit Q_mse (3-bit value pairs across lanes)
+    (40, 32, 8, 200, 4, True),    # 320 groups: more workgroups than the GPU holds at once
+    (80, 28, 4, 100, 4, True),    # GQA 7, 320 groups
 ]
 
 
