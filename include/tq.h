@@ -53,7 +53,8 @@ const char* tq_status_string(int status);
  *    the dim axis contiguous.  For each vector: n = |x|, u = x/n, z = u @ R^T,
  *    code_j = #{i : boundaries[i] < z_j}.  Output vector (b,h,t) is written at
  *    token slot (out_offset + t) of group (b*heads + h), groups `out_cap`
- *    tokens apart.
+ *    tokens apart.  x, rotation and codes 16-byte aligned (TQ_ERR_UNSUPPORTED
+ *    otherwise; so are qjl and signs for tq_quantize_prod).
  */
 int tq_quantize_mse(const uint16_t* x, int batch, int heads, int64_t tokens, int dim,
                     int64_t x_sb, int64_t x_sh, int64_t x_st,

@@ -1,10 +1,7 @@
 // tq_quantize.hip -- TurboQuant encoder kernels for gfx950 (prefill and decode-append).
 //
-// One lane owns one token vector (D = 128): the bf16 vector is held in
-// VGPRs, and the rotation / QJL matrix rows are uniform across the wave, so
-// every multiply-add takes its matrix operand from an SGPR (scalar loads)
-// and its vector operand from a VGPR.  The fp32 evaluation order is fixed
-// (see the reference restatement in the CPU oracle):
+// Every kernel evaluates the encoder in one fixed fp32 order (the CPU oracle restates the
+// reference in the same order), so their outputs are bit-identical to it and to each other:
 //
 //   norm^2 = fma chain d=0..127 of x_d*x_d;  n = sqrt_rn;  n==0 -> 1
 //   u_d    = x_d /_rn n
@@ -13,6 +10,9 @@
 //   Q_prod residual:  khat_d = bf16((fma chain j=0..127 of C[code_j]*R[j][d]) * f32(f16(n)))
 //                     r = x - khat;  rho = sqrt_rn(fma chain r_d^2) (0 -> 1);  rhat = r /_rn rho
 //                     sign_i = (fma chain d of rhat_d*S[i][d]) >= 0
+//
+// Two encoders: the matrix-core kernel for calls of at least MQ_MIN_VECTORS vectors (prefill)
+// and a small-batch kernel with one thread per output index of each vector (decode-append).
 //
 // Reference: runtime/packed_qmse_cache.py:376-402 (_encode_group), :285-310
 // (_encode_keys_qjl_group), :404-435 (_decode_group), :13-43 (_pack_indices),
@@ -26,7 +26,7 @@
 namespace {
 
 constexpr int D = TQ_DIM;
-constexpr int QBLOCK = 256;  // lanes (= vectors) per workgroup
+constexpr int QBLOCK = 256;  // lanes (= vectors) per workgroup of the lane-per-vector decoder
 
 struct QuantArgs {
     const uint16_t* x;
@@ -75,54 +75,6 @@ __device__ __forceinline__ uint32_t bucket_count(float z, const float* __restric
     return c;
 }
 
-// ---- matrix rows through SGPRs, double-buffered
-// Every multiply-add takes its matrix element from an SGPR (the row is uniform across the
-// wave).  Scalar loads return out of order, so a compiler-placed wait for one chunk also
-// waits for any chunk issued after it; the rows are therefore streamed by hand in CH-float
-// chunks through two SGPR buffers: wait for chunk k, issue chunk k + 1, compute on chunk k.
-// Each wait then covers a load that was issued one chunk of compute earlier.  The kernels
-// using this must not spill SGPRs (a spill copy could read a buffer before its wait).
-typedef float sf16 __attribute__((ext_vector_type(16)));
-template <int CH>
-struct SChunk {
-    sf16 a[CH / 16];
-    __device__ __forceinline__ float operator[](int k) const { return a[k >> 4][k & 15]; }
-};
-__device__ __forceinline__ void sload(SChunk<32>& c, const float* p) {
-    asm volatile("s_load_dwordx16 %0, %2, 0x0\n\ts_load_dwordx16 %1, %2, 0x40"
-                 : "=&s"(c.a[0]), "=&s"(c.a[1])
-                 : "s"(p)
-                 : "memory");
-}
-// completes every outstanding scalar load (and LDS access); c is valid afterwards
-__device__ __forceinline__ void swait(SChunk<32>& c) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c.a[0]), "+s"(c.a[1]));
-}
-
-// Streams the D rows of the row-major D x D matrix M (uniform pointer): chunk(d0, C) is
-// called for d0 = 0, CH, 2 CH, ... with C[k] = M[j][d0 + k], then row_end(j).
-template <int CH, typename ChunkFn, typename RowFn>
-__device__ __forceinline__ void stream_rows(const float* M, ChunkFn&& chunk, RowFn&& row_end) {
-    constexpr int NC = D / CH;  // chunks per row (even)
-    SChunk<CH> A, B;
-    sload(A, M);
-    for (int j = 0; j < D; ++j) {
-        const float* mj = M + j * D;
-        const float* next = M + (j + 1 < D ? j + 1 : j) * D;  // the last row reloads itself
-#pragma unroll
-        for (int c = 0; c < NC; c += 2) {
-            swait(A);
-            sload(B, mj + (c + 1) * CH);
-            chunk(c * CH, A);
-            swait(B);
-            sload(A, c + 2 < NC ? mj + (c + 2) * CH : next);
-            chunk((c + 1) * CH, B);
-        }
-        row_end(j);
-    }
-    swait(A);  // no scalar load may still be writing registers the caller reuses
-}
-
 // The same count by binary search over the sorted boundaries (the predicate b[i] < z holds on
 // a prefix): BITS compares, and at level l a select tree over the 2^l candidate thresholds
 // driven by the earlier outcomes (2^BITS - BITS - 1 selects in all, against 2^BITS - 1
@@ -150,146 +102,149 @@ __device__ __forceinline__ uint32_t bucket_search(float z, const float* __restri
     return c;
 }
 
+// ------------------------------------------------------------------ small-batch encoder
+// Below MQ_MIN_VECTORS vectors (decode-append encodes B * Hkv of them per step) a workgroup
+// encodes AV vectors with D threads each: thread (v, j) owns output index j of vector v in
+// every matrix-vector product and runs that output's fma chain alone, in the fixed order
+// above, so the result is bit for bit the chain of the oracle and of the matrix-core kernel.
+// The matrices are staged in LDS with a row stride of MS = 132 floats: thread j reading row j
+// 16 bytes at a time (the rotation and the QJL projection) touches 4 j + 4 k mod 64, distinct
+// banks for the 16 lanes of an LDS pass, and thread d reading column d (the residual decode)
+// touches consecutive banks.  The norms are fma chains over the vector held in LDS, run by
+// every thread of the vector (the same operands in the same order: one value in all of them).
+constexpr int AV = 4;          // vectors per workgroup
+constexpr int AT = AV * D;     // threads per workgroup
+constexpr int MS = D + 4;      // LDS row stride of a staged matrix, floats
+
 template <int BITS, bool PROD>
-__global__ __launch_bounds__(QBLOCK) void quantize_kernel(
+__global__ __launch_bounds__(AT) void append_kernel(
     const uint16_t* __restrict__ x, int heads, int64_t tokens, int64_t n_vec, int64_t x_sb, int64_t x_sh,
     int64_t x_st, const float* __restrict__ R, const float* __restrict__ centers,
     const float* __restrict__ boundaries, const float* __restrict__ S, uint8_t* __restrict__ codes,
     uint16_t* __restrict__ norms, uint8_t* __restrict__ signs, uint16_t* __restrict__ rnorms, int64_t out_cap,
     int64_t out_offset) {
-    __shared__ uint8_t s_code[D][QBLOCK];  // PROD only: codes of each lane, column per lane
-    __shared__ float s_centers[1 << BITS];
-    if (PROD && threadIdx.x < (1 << BITS)) s_centers[threadIdx.x] = centers[threadIdx.x];
-    if (PROD) __syncthreads();
+    __shared__ float4 sR[D * MS / 4];
+    __shared__ float4 sS[PROD ? D * MS / 4 : 1];
+    __shared__ float4 sx[AV][D / 4];    // the vector in fp32, later rhat
+    __shared__ float4 su[AV][D / 4];    // u = x / n, later the residual
+    __shared__ float4 sc[AV][D / 4];    // C[code_j]
+    __shared__ uint8_t scode[AV][D];
+    __shared__ float scent[1 << BITS];
 
-    const int64_t v = (int64_t)blockIdx.x * QBLOCK + threadIdx.x;
-    if (v >= n_vec) return;  // no barrier below this point
-    const int64_t t = v % tokens;
-    const int64_t gh = v / tokens;
-    const int64_t h = gh % heads;
-    const int64_t b = gh / heads;
-    const uint16_t* xv = x + b * x_sb + h * x_sh + t * x_st;
-    const int64_t slot = gh * out_cap + out_offset + t;
+    const int tid = threadIdx.x;
+    const int vi = tid / D, j = tid % D;  // vector of the workgroup (two whole waves), output index
+    const int64_t v = (int64_t)blockIdx.x * AV + vi;
+    const bool active = v < n_vec;        // threads of missing vectors compute on unused LDS, store nothing
+    float* const fx = reinterpret_cast<float*>(sx[vi]);
+    float* const fu = reinterpret_cast<float*>(su[vi]);
+    float* const fc = reinterpret_cast<float*>(sc[vi]);
 
-    // ---- load x, norm
-    const uint4* x4 = reinterpret_cast<const uint4*>(xv);
-    auto unpack8 = [](const uint4& w, float* o) {
-        o[0] = tq::bf16_to_f32(w.x & 0xFFFFu);
-        o[1] = tq::bf16_to_f32(w.x >> 16);
-        o[2] = tq::bf16_to_f32(w.y & 0xFFFFu);
-        o[3] = tq::bf16_to_f32(w.y >> 16);
-        o[4] = tq::bf16_to_f32(w.z & 0xFFFFu);
-        o[5] = tq::bf16_to_f32(w.z >> 16);
-        o[6] = tq::bf16_to_f32(w.w & 0xFFFFu);
-        o[7] = tq::bf16_to_f32(w.w >> 16);
-    };
-    float u[D];
+    // ---- the vector, the codebook and the matrices into LDS (row r of a matrix at r * MS)
+    int64_t slot = 0;
+    if (active) {
+        const int64_t t = v % tokens, gh = v / tokens;
+        const int64_t h = gh % heads, b = gh / heads;
+        fx[j] = tq::bf16_to_f32(x[b * x_sb + h * x_sh + t * x_st + j]);
+        slot = gh * out_cap + out_offset + t;
+    }
+    if (PROD && tid < (1 << BITS)) scent[tid] = centers[tid];
+    for (int k = tid; k < D * D / 4; k += AT) {
+        const int r = k / (D / 4), c4 = k % (D / 4);
+        sR[r * (MS / 4) + c4] = reinterpret_cast<const float4*>(R)[k];
+        if constexpr (PROD) sS[r * (MS / 4) + c4] = reinterpret_cast<const float4*>(S)[k];
+    }
+    __syncthreads();
+
+    // ---- norm, u = x / n
     float ss = 0.0f;
-    if constexpr (PROD) {
-        // the norm from one streamed pass over x, then x read again into u / n: the raw vector
-        // and u are never live together (keeps the Q_prod kernel at three waves per SIMD)
 #pragma unroll
-        for (int i = 0; i < D / 8; ++i) {
-            float e[8];
-            unpack8(x4[i], e);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(e[k], e[k], ss);
-        }
-        __asm__ volatile("" ::: "memory");  // a second read, not a copy held from the first
-    } else {
-#pragma unroll
-        for (int i = 0; i < D / 8; ++i) unpack8(x4[i], &u[8 * i]);
-#pragma unroll
-        for (int d = 0; d < D; ++d) ss = __builtin_fmaf(u[d], u[d], ss);
+    for (int d4 = 0; d4 < D / 4; ++d4) {
+        const float4 e = sx[vi][d4];
+        ss = __builtin_fmaf(e.x, e.x, ss);
+        ss = __builtin_fmaf(e.y, e.y, ss);
+        ss = __builtin_fmaf(e.z, e.z, ss);
+        ss = __builtin_fmaf(e.w, e.w, ss);
     }
     float n = tq::sqrt_rn(ss);
     if (!(n > 0.0f)) n = 1.0f;
-    if constexpr (PROD) {
-#pragma unroll
-        for (int i = 0; i < D / 8; ++i) {
-            unpack8(x4[i], &u[8 * i]);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) u[8 * i + k] = tq::div_rn(u[8 * i + k], n);
-        }
-    } else {
-#pragma unroll
-        for (int d = 0; d < D; ++d) u[d] = tq::div_rn(u[d], n);
-    }
+    const float xj = fx[j];
+    fu[j] = tq::div_rn(xj, n);
     const uint32_t n16 = tq::f32_to_f16(n);
-    norms[slot] = (uint16_t)n16;
+    if (active && j == 0) norms[slot] = (uint16_t)n16;
+    __syncthreads();
 
-    // ---- rotate, bucketize, pack
-    constexpr int NB = (1 << BITS) - 1;
-    constexpr int ROW = D * BITS / 8;
-    uint32_t* crow = reinterpret_cast<uint32_t*>(codes + slot * ROW);
-    BitWriter bw;
-    if constexpr (PROD) {
-        for (int j = 0; j < D; ++j) {
-            const float* rj = R + j * D;
-            float z = 0.0f;
-#pragma unroll
-            for (int d = 0; d < D; ++d) z = __builtin_fmaf(u[d], rj[d], z);
-            const uint32_t c = bucket_search<BITS>(z, boundaries);
-            bw.put(c, BITS, crow);
-            s_code[j][threadIdx.x] = (uint8_t)c;
-        }
-    } else {
+    // ---- z_j = fma chain d of u_d R[j][d]; code_j
     float z = 0.0f;
-    constexpr int CH = 32;
-    stream_rows<CH>(
-        R,
-        [&](int d0, const SChunk<CH>& C) {
+    {
+        const float4* rj = sR + j * (MS / 4);
 #pragma unroll
-            for (int k = 0; k < CH; ++k) z = __builtin_fmaf(u[d0 + k], C[k], z);
-        },
-        [&](int j) {
-            const uint32_t c = bucket_count<NB>(z, boundaries);
-            z = 0.0f;
-            bw.put(c, BITS, crow);
-        });
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+            const float4 uu = su[vi][d4], rr = rj[d4];
+            z = __builtin_fmaf(uu.x, rr.x, z);
+            z = __builtin_fmaf(uu.y, rr.y, z);
+            z = __builtin_fmaf(uu.z, rr.z, z);
+            z = __builtin_fmaf(uu.w, rr.w, z);
+        }
+    }
+    const uint32_t code = bucket_count<(1 << BITS) - 1>(z, boundaries);
+    scode[vi][j] = (uint8_t)code;
+    if constexpr (PROD) fc[j] = scent[code];
+    __syncthreads();
+
+    // ---- the code row: thread j < ROW / 4 assembles dword j (stream bits [32 j, 32 j + 32))
+    constexpr int ROW = D * BITS / 8;
+    if (active && j < ROW / 4) {
+        const int b0 = 32 * j;
+        uint64_t acc = 0;
+        for (int k = b0 / BITS; k <= (b0 + 31) / BITS; ++k)
+            acc |= (uint64_t)scode[vi][k] << (k * BITS - b0 + 32);  // shift in [33 - BITS, 63]
+        reinterpret_cast<uint32_t*>(codes + slot * ROW)[j] = (uint32_t)(acc >> 32);
     }
 
     if constexpr (PROD) {
-        // ---- residual decode khat = bf16((C[code] @ R) * f32(f16(n))), accumulated row by row
-        float* acc = u;  // u is dead after the rotation: one 128-register array
+        // ---- residual: khat_d = bf16((fma chain jj of C[code_jj] R[jj][d]) * f32(f16(n))), d = j
+        const float* fR = reinterpret_cast<const float*>(sR);
+        float acc = 0.0f;
 #pragma unroll
-        for (int d = 0; d < D; ++d) acc[d] = 0.0f;
-        for (int j = 0; j < D; ++j) {
-            const float cj = s_centers[s_code[j][threadIdx.x]];
-            const float* rj = R + j * D;
-#pragma unroll
-            for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
+        for (int k4 = 0; k4 < D / 4; ++k4) {
+            const float4 cc = sc[vi][k4];
+            acc = __builtin_fmaf(cc.x, fR[(4 * k4 + 0) * MS + j], acc);
+            acc = __builtin_fmaf(cc.y, fR[(4 * k4 + 1) * MS + j], acc);
+            acc = __builtin_fmaf(cc.z, fR[(4 * k4 + 2) * MS + j], acc);
+            acc = __builtin_fmaf(cc.w, fR[(4 * k4 + 3) * MS + j], acc);
         }
-        const float nf = tq::f16_to_f32(n16);
-        __asm__ volatile("" ::: "memory");  // x is re-read here, not held across the loop above
+        const float kh = tq::bf16_to_f32(tq::f32_to_bf16(acc * tq::f16_to_f32(n16)));
+        const float r = xj - kh;
+        fu[j] = r;  // u was last read by the rotation, before the barrier above
+        __syncthreads();
         float rs = 0.0f;
 #pragma unroll
-        for (int i = 0; i < D / 8; ++i) {
-            uint4 w = x4[i];
-            uint32_t xs[8] = {w.x & 0xFFFFu, w.x >> 16, w.y & 0xFFFFu, w.y >> 16,
-                              w.z & 0xFFFFu, w.z >> 16, w.w & 0xFFFFu, w.w >> 16};
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int d = 8 * i + k;
-                const float kh = tq::bf16_to_f32(tq::f32_to_bf16(acc[d] * nf));
-                acc[d] = tq::bf16_to_f32(xs[k]) - kh;
-                rs = __builtin_fmaf(acc[d], acc[d], rs);
-            }
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+            const float4 e = su[vi][d4];
+            rs = __builtin_fmaf(e.x, e.x, rs);
+            rs = __builtin_fmaf(e.y, e.y, rs);
+            rs = __builtin_fmaf(e.z, e.z, rs);
+            rs = __builtin_fmaf(e.w, e.w, rs);
         }
         float rho = tq::sqrt_rn(rs);
         if (!(rho > 0.0f)) rho = 1.0f;
+        fx[j] = tq::div_rn(r, rho);  // x was last read before the first barrier
+        if (active && j == 0) rnorms[slot] = (uint16_t)tq::f32_to_f16(rho);
+        __syncthreads();
+        // ---- sign_i = (fma chain d of rhat_d S[i][d]) >= 0, i = j; a wave holds 64 of them
+        float p = 0.0f;
+        const float4* si = sS + j * (MS / 4);
 #pragma unroll
-        for (int d = 0; d < D; ++d) acc[d] = tq::div_rn(acc[d], rho);
-        rnorms[slot] = (uint16_t)tq::f32_to_f16(rho);
-        uint32_t* srow = reinterpret_cast<uint32_t*>(signs + slot * (D / 8));
-        BitWriter sw;
-        for (int i = 0; i < D; ++i) {
-            const float* si = S + i * D;
-            float p = 0.0f;
-#pragma unroll
-            for (int d = 0; d < D; ++d) p = __builtin_fmaf(acc[d], si[d], p);
-            sw.put(p >= 0.0f ? 1u : 0u, 1, srow);
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+            const float4 hh = sx[vi][d4], ww = si[d4];
+            p = __builtin_fmaf(hh.x, ww.x, p);
+            p = __builtin_fmaf(hh.y, ww.y, p);
+            p = __builtin_fmaf(hh.z, ww.z, p);
+            p = __builtin_fmaf(hh.w, ww.w, p);
         }
+        const uint64_t sb = __builtin_amdgcn_ballot_w64(p >= 0.0f);  // bit l: index 64 (j / 64) + l
+        if (active && (j & 63) == 0)
+            reinterpret_cast<uint2*>(signs + slot * (D / 8))[j >> 6] = make_uint2((uint32_t)sb, (uint32_t)(sb >> 32));
     }
 }
 
@@ -320,7 +275,7 @@ __global__ __launch_bounds__(QBLOCK) void quantize_kernel(
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int MQ_WAVES = 8;                 // waves per workgroup, each on its own tiles
 constexpr int MQ_THREADS = 64 * MQ_WAVES;
-constexpr int64_t MQ_MIN_VECTORS = 4096;    // below this the lane-per-vector kernel is used
+constexpr int64_t MQ_MIN_VECTORS = 4096;    // below this the small-batch encoder is used
 constexpr int LUT_MAX = 512;                // cells of the bucketize grid
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
@@ -792,9 +747,9 @@ int launch_quantize(const QuantArgs& a, hipStream_t s) {
         TQ_CHECK_LAUNCH();
         return TQ_OK;
     }
-    const int64_t blocks = (a.n_vec + QBLOCK - 1) / QBLOCK;
+    const int64_t blocks = (a.n_vec + AV - 1) / AV;
     if (blocks == 0) return TQ_OK;
-    hipLaunchKernelGGL((quantize_kernel<BITS, PROD>), dim3((unsigned)blocks), dim3(QBLOCK), 0, s, a.x, a.heads,
+    hipLaunchKernelGGL((append_kernel<BITS, PROD>), dim3((unsigned)blocks), dim3(AT), 0, s, a.x, a.heads,
                        a.tokens, a.n_vec, a.x_sb, a.x_sh, a.x_st, a.R, a.centers, a.boundaries, a.S, a.codes,
                        a.norms, a.signs, a.rnorms, a.out_cap, a.out_offset);
     TQ_CHECK_LAUNCH();
@@ -810,7 +765,7 @@ extern "C" int tq_quantize_mse(const uint16_t* x, int batch, int heads, int64_t 
     int st = check_common(x, batch, heads, tokens, dim, x_sb, x_sh, x_st, out_cap, out_offset);
     if (st != TQ_OK) return st;
     if (!rotation || !boundaries || !codes || !norms) return TQ_ERR_INVALID_ARGUMENT;
-    if (!aligned16(codes)) return TQ_ERR_UNSUPPORTED;
+    if (!aligned16(codes) || !aligned16(rotation)) return TQ_ERR_UNSUPPORTED;
     QuantArgs a{x, heads, tokens, (int64_t)batch * heads * tokens, x_sb, x_sh, x_st, rotation, nullptr,
                 boundaries, nullptr, codes, norms, nullptr, nullptr, out_cap, out_offset};
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -832,7 +787,7 @@ extern "C" int tq_quantize_prod(const uint16_t* x, int batch, int heads, int64_t
     if (st != TQ_OK) return st;
     if (!rotation || !centers || !boundaries || !qjl || !codes || !norms || !signs || !rnorms)
         return TQ_ERR_INVALID_ARGUMENT;
-    if (!aligned16(codes) || !aligned16(signs)) return TQ_ERR_UNSUPPORTED;
+    if (!aligned16(codes) || !aligned16(signs) || !aligned16(rotation) || !aligned16(qjl)) return TQ_ERR_UNSUPPORTED;
     QuantArgs a{x, heads, tokens, (int64_t)batch * heads * tokens, x_sb, x_sh, x_st, rotation, centers,
                 boundaries, qjl, codes, norms, signs, rnorms, out_cap, out_offset};
     hipStream_t s = static_cast<hipStream_t>(stream);
