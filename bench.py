@@ -368,6 +368,75 @@ def bench_host(args, dev) -> dict:
             "calls": out}
 
 
+def bench_append(args, dev) -> dict:
+    """Decode-append: the encoders on one new token per (batch row, KV head), writing in place
+    at a slot of a capacity buffer, as a decode step does for every packed layer.  K (Q_prod or
+    Q_mse) and V (Q_mse) per layer, timed eagerly (launch included) and as a HIP graph of
+    `--layers` layers (device time)."""
+    import torch
+
+    from turboquant.runtime import kernels as K
+    from turboquant.runtime.params import layer_codecs
+    from turboquant.runtime.synthetic import kv_bf16
+
+    B, Hkv, D, bits, cap = args.batch, args.kv_heads, 128, args.bits, 64
+    qjl = not args.no_qjl
+    lc = layer_codecs(D, bits, 0, qjl, dev)
+    kb = lc.key_bits
+    buf = {"kc": torch.zeros(B, Hkv, cap, K.row_bytes(D, kb), dtype=torch.uint8, device=dev),
+           "kn": torch.zeros(B, Hkv, cap, dtype=torch.float16, device=dev),
+           "ks": torch.zeros(B, Hkv, cap, D // 8, dtype=torch.uint8, device=dev),
+           "kr": torch.zeros(B, Hkv, cap, dtype=torch.float16, device=dev),
+           "vc": torch.zeros(B, Hkv, cap, K.row_bytes(D, bits), dtype=torch.uint8, device=dev),
+           "vn": torch.zeros(B, Hkv, cap, dtype=torch.float16, device=dev)}
+    k = kv_bf16((B, Hkv, 1, D), seed=1, device=dev)
+    v = kv_bf16((B, Hkv, 1, D), seed=2, device=dev)
+
+    def enc_k(slot):
+        if qjl:
+            K.quantize_prod(k, lc.key, lc.qjl, buf["kc"], buf["kn"], buf["ks"], buf["kr"], offset=slot)
+        else:
+            K.quantize_mse(k, lc.key, buf["kc"], buf["kn"], offset=slot)
+
+    def enc_v(slot):
+        K.quantize_mse(v, lc.value, buf["vc"], buf["vn"], offset=slot)
+
+    def eager_us(fn, reps=400):
+        for i in range(20):
+            fn(i % cap)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(reps):
+            fn(i % cap)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    k_us, v_us = eager_us(enc_k), eager_us(enc_v)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for li in range(args.layers):
+            enc_k(li % cap)
+            enc_v(li % cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    layer_us = e0.elapsed_time(e1) * 1e3 / (args.steps * args.layers)
+    return {"metric": "decode-append encode, K + V per layer and decode step", "value": round(layer_us, 2),
+            "unit": "us", "higher_is_better": False,
+            "config": {"workload": f"one token per (batch row, KV head): B={B}, Hkv={Hkv}, {bits}-bit "
+                                   f"{'Q_prod' if qjl else 'Q_mse'} keys, {bits}-bit Q_mse values",
+                       "vectors_per_call": B * Hkv},
+            "graph_layers": args.layers, "steps": args.steps,
+            "eager_us_per_call": {"keys": round(k_us, 2), "values": round(v_us, 2)}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -394,6 +463,8 @@ def main() -> int:
     ap.add_argument("--c5-new", type=int, default=512)
     ap.add_argument("--host", action="store_true",
                     help="host cost per decode-attention call (Python wrappers) instead of the C2 line")
+    ap.add_argument("--append", action="store_true",
+                    help="decode-append encoders (one new token per batch row and KV head) instead of the C2 line")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -420,6 +491,9 @@ def main() -> int:
         return 0
     if args.host:
         print(json.dumps(bench_host(args, dev)))
+        return 0
+    if args.append:
+        print(json.dumps(bench_append(args, dev)))
         return 0
     B, Hq, Hkv, N, D, bits = args.batch, args.q_heads, args.kv_heads, args.context, 128, args.bits
     qjl = not args.no_qjl
