@@ -182,7 +182,7 @@ int tq_group_matrix(const float* sub, int sub_dim, const int32_t* channels, int 
  * `bits` MSE bits plus the QJL sketch (centers, signs and rnorms then required).
  * Results are those of tq_quantize_mse / tq_quantize_prod applied to the gathered
  * sub-vectors x[..., channels] with D = sub_dim.  rotation and qjl are the channel-space
- * [dim][dim] matrices of tq_group_matrix (device memory).
+ * [dim][dim] matrices of tq_group_matrix (device memory, 16-byte aligned).
  * Replaces reference _encode_split (runtime/packed_qmse_cache.py:481-496) and
  * _encode_keys_split_qjl (:437-454), one group per call.
  */

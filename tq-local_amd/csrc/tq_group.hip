@@ -178,6 +178,147 @@ __global__ __launch_bounds__(GBLOCK) void quantize_group_kernel(
     }
 }
 
+// Decode-append sizes (below GQ_SMALL vectors): a workgroup encodes GAV vectors with D threads
+// each.  Thread (v, j) runs output j's chains of vector v -- z_j and p_j for j < d, khat_j for
+// every channel j -- and every thread of a vector runs the two norm chains over the masked row
+// held in LDS (the same operands in the same order: one value in all of them).  These are the
+// lane kernel's chains term for term, so the outputs are bit-identical to it.  The channel-space
+// matrices are staged in LDS with a row stride of GMS = 132 floats (rows read 16 bytes at a time
+// and columns read one float at a time both spread over the banks).
+constexpr int GAV = 4;                 // vectors per workgroup
+constexpr int GAT = GAV * D;           // threads per workgroup
+constexpr int GMS = D + 4;             // LDS row stride of a staged matrix, floats
+constexpr int64_t GQ_SMALL = 8192;     // below this many vectors the small-batch kernel runs
+
+template <bool PROD>
+__global__ __launch_bounds__(GAT) void quantize_group_small_kernel(
+    const uint16_t* __restrict__ x, int heads, int64_t tokens, int64_t n_vec, int64_t x_sb, int64_t x_sh,
+    int64_t x_st, ChanMask mask, int sub_dim, int bits, const float* __restrict__ R,
+    const float* __restrict__ centers, const float* __restrict__ boundaries, const float* __restrict__ S,
+    uint8_t* __restrict__ codes, uint16_t* __restrict__ norms, uint8_t* __restrict__ signs,
+    uint16_t* __restrict__ rnorms, int64_t out_cap, int64_t out_offset) {
+    __shared__ float4 sR[D * GMS / 4];
+    __shared__ float4 sS[PROD ? D * GMS / 4 : 1];
+    __shared__ float4 sx[GAV][D / 4];   // the masked vector, later rhat
+    __shared__ float4 su[GAV][D / 4];   // u = x / n, later the residual
+    __shared__ float sc[GAV][D];        // C[code_j], j < d
+    __shared__ uint8_t scode[GAV][D];
+    __shared__ float s_bound[(1 << MAX_BITS) - 1];
+    __shared__ float s_centers[PROD ? (1 << MAX_BITS) : 1];
+
+    const int tid = threadIdx.x;
+    const int vi = tid / D, j = tid % D;  // vector of the workgroup (two whole waves), output index
+    const int64_t v = (int64_t)blockIdx.x * GAV + vi;
+    const bool active = v < n_vec;        // threads of missing vectors compute on unused LDS, store nothing
+    float* const fx = reinterpret_cast<float*>(sx[vi]);
+    float* const fu = reinterpret_cast<float*>(su[vi]);
+    const int nb = (1 << bits) - 1;
+    for (int i = tid; i < nb; i += GAT) s_bound[i] = boundaries[i];
+    if (PROD)
+        for (int i = tid; i <= nb; i += GAT) s_centers[i] = centers[i];
+
+    int64_t slot = 0;
+    if (active) {
+        const int64_t t = v % tokens, gh = v / tokens;
+        const int64_t h = gh % heads, b = gh / heads;
+        const uint32_t mw = j < 32 ? mask.w[0] : j < 64 ? mask.w[1] : j < 96 ? mask.w[2] : mask.w[3];
+        fx[j] = ((mw >> (j & 31)) & 1u) ? tq::bf16_to_f32(x[b * x_sb + h * x_sh + t * x_st + j]) : 0.0f;
+        slot = gh * out_cap + out_offset + t;
+    }
+    for (int k = tid; k < D * D / 4; k += GAT) {
+        const int r = k / (D / 4), c4 = k % (D / 4);
+        sR[r * (GMS / 4) + c4] = reinterpret_cast<const float4*>(R)[k];
+        if constexpr (PROD) sS[r * (GMS / 4) + c4] = reinterpret_cast<const float4*>(S)[k];
+    }
+    __syncthreads();
+
+    // ---- norm of the group's sub-vector, u = x / n
+    float ss = 0.0f;
+#pragma unroll
+    for (int d4 = 0; d4 < D / 4; ++d4) {
+        const float4 e = sx[vi][d4];
+        ss = __builtin_fmaf(e.x, e.x, ss);
+        ss = __builtin_fmaf(e.y, e.y, ss);
+        ss = __builtin_fmaf(e.z, e.z, ss);
+        ss = __builtin_fmaf(e.w, e.w, ss);
+    }
+    float n = tq::sqrt_rn(ss);
+    if (!(n > 0.0f)) n = 1.0f;
+    const float xj = fx[j];
+    fu[j] = tq::div_rn(xj, n);
+    const uint32_t n16 = tq::f32_to_f16(n);
+    if (active && j == 0) norms[slot] = (uint16_t)n16;
+    __syncthreads();
+
+    // ---- z_j (rows j < d), code_j
+    float z = 0.0f;
+    {
+        const float4* rj = sR + j * (GMS / 4);
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+            const float4 uu = su[vi][d4], rr = rj[d4];
+            z = __builtin_fmaf(uu.x, rr.x, z);
+            z = __builtin_fmaf(uu.y, rr.y, z);
+            z = __builtin_fmaf(uu.z, rr.z, z);
+            z = __builtin_fmaf(uu.w, rr.w, z);
+        }
+    }
+    const uint32_t code = j < sub_dim ? bucket_lds(z, s_bound, bits) : 0u;
+    scode[vi][j] = (uint8_t)code;
+    if constexpr (PROD) sc[vi][j] = s_centers[code];
+    __syncthreads();
+
+    // ---- the code row, ceil(d bits / 8) bytes: thread j builds byte j (stream bits [8 j, 8 j + 8))
+    const int rb = (sub_dim * bits + 7) >> 3;
+    if (active && j < rb) {
+        const int b0 = 8 * j;
+        const int k1 = (b0 + 7) / bits < sub_dim - 1 ? (b0 + 7) / bits : sub_dim - 1;
+        uint32_t acc = 0;
+        for (int k = b0 / bits; k <= k1; ++k) acc |= (uint32_t)scode[vi][k] << (k * bits - b0 + 8);  // shift in [9 - bits, 15]
+        codes[slot * rb + j] = (uint8_t)(acc >> 8);
+    }
+
+    if constexpr (PROD) {
+        // ---- residual: khat_c = bf16((fma chain jj < d of C[code_jj] R[jj][c]) * f32(f16(n))), c = j
+        const float* fR = reinterpret_cast<const float*>(sR);
+        float acc = 0.0f;
+        for (int jj = 0; jj < sub_dim; ++jj) acc = __builtin_fmaf(sc[vi][jj], fR[jj * GMS + j], acc);
+        const float kh = tq::bf16_to_f32(tq::f32_to_bf16(acc * tq::f16_to_f32(n16)));
+        const float r = xj - kh;  // 0 - 0 outside the group: R's columns there are zero
+        fu[j] = r;                // u was last read by the rotation, before the barrier above
+        __syncthreads();
+        float rs = 0.0f;
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+            const float4 e = su[vi][d4];
+            rs = __builtin_fmaf(e.x, e.x, rs);
+            rs = __builtin_fmaf(e.y, e.y, rs);
+            rs = __builtin_fmaf(e.z, e.z, rs);
+            rs = __builtin_fmaf(e.w, e.w, rs);
+        }
+        float rho = tq::sqrt_rn(rs);
+        if (!(rho > 0.0f)) rho = 1.0f;
+        fx[j] = tq::div_rn(r, rho);  // x was last read before the first barrier
+        if (active && j == 0) rnorms[slot] = (uint16_t)tq::f32_to_f16(rho);
+        __syncthreads();
+        // ---- sign_i (i = j < d): fma chain over the channels of rhat_c S[i][c]
+        float p = 0.0f;
+        const float4* si = sS + j * (GMS / 4);
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+            const float4 hh = sx[vi][d4], ww = si[d4];
+            p = __builtin_fmaf(hh.x, ww.x, p);
+            p = __builtin_fmaf(hh.y, ww.y, p);
+            p = __builtin_fmaf(hh.z, ww.z, p);
+            p = __builtin_fmaf(hh.w, ww.w, p);
+        }
+        const uint64_t sb = __builtin_amdgcn_ballot_w64(j < sub_dim && p >= 0.0f);  // bit l: index 64 (j / 64) + l
+        const int l = j & 63, byte = 8 * (j >> 6) + l;  // lanes 0..7 of a wave write its 8 bytes
+        if (active && l < 8 && byte < ((sub_dim + 7) >> 3))
+            signs[slot * ((sub_dim + 7) >> 3) + byte] = (uint8_t)(sb >> (8 * l));
+    }
+}
+
 // out = bf16((C[code] @ R) * f32(norm)) on the group's channels; with QJL (Q_prod keys)
 // corr = bf16(((s @ S) * rnorm) * qs), out = bf16(f32(khat) + f32(corr)).  Channels
 // outside the group are zeroed, or kept from `out` when `merge` is set.
@@ -306,9 +447,23 @@ extern "C" int tq_quantize_group(const uint16_t* x, int batch, int heads, int64_
     if (prod && (!centers || !signs || !rnorms)) return TQ_ERR_INVALID_ARGUMENT;
     if (!aligned16(x) || (x_sb % 8) || (x_sh % 8) || (x_st % 8)) return TQ_ERR_UNSUPPORTED;
     const int64_t n_vec = (int64_t)batch * heads * tokens;
-    const int64_t blocks = (n_vec + GBLOCK - 1) / GBLOCK;
-    if (blocks == 0) return TQ_OK;
+    if (n_vec == 0) return TQ_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!aligned16(rotation) || (prod && !aligned16(qjl))) return TQ_ERR_UNSUPPORTED;
+    if (n_vec < GQ_SMALL) {
+        const int64_t sblocks = (n_vec + GAV - 1) / GAV;
+        if (prod)
+            hipLaunchKernelGGL((quantize_group_small_kernel<true>), dim3((unsigned)sblocks), dim3(GAT), 0, s, x,
+                               heads, tokens, n_vec, x_sb, x_sh, x_st, mask, sub_dim, bits, rotation, centers,
+                               boundaries, qjl, codes, norms, signs, rnorms, out_cap, out_offset);
+        else
+            hipLaunchKernelGGL((quantize_group_small_kernel<false>), dim3((unsigned)sblocks), dim3(GAT), 0, s, x,
+                               heads, tokens, n_vec, x_sb, x_sh, x_st, mask, sub_dim, bits, rotation, nullptr,
+                               boundaries, nullptr, codes, norms, nullptr, nullptr, out_cap, out_offset);
+        TQ_CHECK_LAUNCH();
+        return TQ_OK;
+    }
+    const int64_t blocks = (n_vec + GBLOCK - 1) / GBLOCK;
     if (prod)
         hipLaunchKernelGGL((quantize_group_kernel<true>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, x, heads,
                            tokens, n_vec, x_sb, x_sh, x_st, mask, sub_dim, bits, rotation, centers, boundaries, qjl,
