@@ -401,6 +401,36 @@ def bench_append(args, dev) -> dict:
     def enc_v(slot):
         K.quantize_mse(v, lc.value, buf["vc"], buf["vn"], offset=slot)
 
+    if args.outliers:
+        # outlier-split layers: both channel groups, the first --outliers channels as the outlier
+        # group (the split's encoders take any sorted channel subset; which ones does not change
+        # the work), the outlier group one bit wider
+        import numpy as np
+
+        from turboquant.runtime.params import split_codecs
+
+        outl = np.arange(args.outliers)
+        sc = split_codecs(np.arange(args.outliers, D), outl, bits, 1, 0, qjl, dev)
+
+        def group_bufs(g, prod):
+            b = [torch.zeros(B, Hkv, cap, K.row_bytes(g.dim, g.bits), dtype=torch.uint8, device=dev),
+                 torch.zeros(B, Hkv, cap, dtype=torch.float16, device=dev)]
+            if prod:
+                b += [torch.zeros(B, Hkv, cap, K.row_bytes(g.dim, 1), dtype=torch.uint8, device=dev),
+                      torch.zeros(B, Hkv, cap, dtype=torch.float16, device=dev)]
+            return b
+
+        kgroups = [(g, group_bufs(g, qjl)) for g in (sc.key_normal, sc.key_outlier)]
+        vgroups = [(g, group_bufs(g, False)) for g in (sc.value_normal, sc.value_outlier)]
+
+        def enc_k(slot):  # noqa: F811
+            for g, b in kgroups:
+                K.quantize_group(k, g, *b, offset=slot)
+
+        def enc_v(slot):  # noqa: F811
+            for g, b in vgroups:
+                K.quantize_group(v, g, *b, offset=slot)
+
     def eager_us(fn, reps=400):
         for i in range(20):
             fn(i % cap)
@@ -431,7 +461,9 @@ def bench_append(args, dev) -> dict:
     return {"metric": "decode-append encode, K + V per layer and decode step", "value": round(layer_us, 2),
             "unit": "us", "higher_is_better": False,
             "config": {"workload": f"one token per (batch row, KV head): B={B}, Hkv={Hkv}, {bits}-bit "
-                                   f"{'Q_prod' if qjl else 'Q_mse'} keys, {bits}-bit Q_mse values",
+                                   f"{'Q_prod' if qjl else 'Q_mse'} keys, {bits}-bit Q_mse values"
+                                   + (f", outlier split ({args.outliers} channels at {bits + 1} bits; "
+                                      "both groups of K and of V)" if args.outliers else ""),
                        "vectors_per_call": B * Hkv},
             "graph_layers": args.layers, "steps": args.steps,
             "eager_us_per_call": {"keys": round(k_us, 2), "values": round(v_us, 2)}}
@@ -483,6 +515,9 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.append:
+        print(json.dumps(bench_append(args, dev)))
+        return 0
     if args.outliers:
         print(json.dumps(bench_split(args, dev)))
         return 0
@@ -491,9 +526,6 @@ def main() -> int:
         return 0
     if args.host:
         print(json.dumps(bench_host(args, dev)))
-        return 0
-    if args.append:
-        print(json.dumps(bench_append(args, dev)))
         return 0
     B, Hq, Hkv, N, D, bits = args.batch, args.q_heads, args.kv_heads, args.context, 128, args.bits
     qjl = not args.no_qjl
