@@ -187,6 +187,40 @@ def test_quantize_strided_input_and_decode_append(cuda):
     assert np.array_equal(u16(bufs[3]).reshape(-1), rr)
 
 
+@pytest.mark.parametrize("bits,prod", [(1, False), (3, False), (4, False), (2, True), (4, True)])
+def test_small_batch_and_matrix_core_encoders_agree(cuda, bits, prod):
+    """The same 4096 vectors encoded by one call (the matrix-core kernel, 4096 and up) and by
+    two calls of 4095 and 1 vectors (the small-batch kernel) are bit-identical: codes, norms,
+    and for Q_prod signs and residual norms."""
+    B, H, T = 4, 8, 128  # 4096 vectors
+    x = kv_bf16((B, H, T, D), seed=60 + bits, device=cuda).reshape(1, 1, B * H * T, D)
+    lc = layer_codecs(D, bits, 0, prod, cuda)
+    codec = lc.key if prod else lc.value
+    n = x.shape[2]
+
+    def bufs():
+        b = [torch.zeros(1, 1, n, K.row_bytes(D, codec.bits), dtype=torch.uint8, device=cuda),
+             torch.zeros(1, 1, n, dtype=torch.float16, device=cuda)]
+        if prod:
+            b += [torch.zeros(1, 1, n, D // 8, dtype=torch.uint8, device=cuda),
+                  torch.zeros(1, 1, n, dtype=torch.float16, device=cuda)]
+        return b
+
+    def enc(xs, b, off):
+        if prod:
+            K.quantize_prod(xs, codec, lc.qjl, *b, offset=off)
+        else:
+            K.quantize_mse(xs, codec, *b, offset=off)
+
+    whole, parts = bufs(), bufs()
+    enc(x, whole, 0)
+    enc(x[:, :, :n - 1], parts, 0)
+    enc(x[:, :, n - 1:], parts, n - 1)
+    torch.cuda.synchronize()
+    for a, b in zip(whole, parts):
+        assert torch.equal(a, b)
+
+
 def test_quantize_full_size_c2_subsample(cuda):
     """BASELINE config 2 key layer (B=8, Hkv=8, N=32768, 4-bit Q_prod): a random
     2048-vector subsample is bit-exact against the oracle; the whole layer

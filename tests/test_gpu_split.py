@@ -94,6 +94,34 @@ def test_quantize_group_prod_bit_exact(cuda, d, bits, extra):
         assert np.array_equal(u16(rnorms).reshape(-1), rr)
 
 
+@pytest.mark.parametrize("prod", [False, True])
+def test_group_small_batch_and_lane_encoders_agree(cuda, prod):
+    """One group of 8192 vectors encoded by one call (the lane-per-vector kernel, 8192 and up) and
+    by calls of 8191 and 1 vectors (the small-batch kernel) is bit-identical."""
+    outl = _channels(13, 5)
+    sc = split_codecs(np.setdiff1d(np.arange(D), outl), outl, 3, 2, 0, True, cuda)
+    g = sc.key_outlier if prod else sc.value_normal
+    x = _with_specials(kv_bf16((1, 1, 8187, D), seed=77, device=cuda), outl)
+    n = x.shape[2]
+    assert n == 8192
+
+    def bufs():
+        b = [torch.zeros(1, 1, n, K.row_bytes(g.dim, g.bits), dtype=torch.uint8, device=cuda),
+             torch.zeros(1, 1, n, dtype=torch.float16, device=cuda)]
+        if prod:
+            b += [torch.zeros(1, 1, n, K.row_bytes(g.dim, 1), dtype=torch.uint8, device=cuda),
+                  torch.zeros(1, 1, n, dtype=torch.float16, device=cuda)]
+        return b
+
+    whole, parts = bufs(), bufs()
+    K.quantize_group(x, g, *whole)
+    K.quantize_group(x[:, :, :n - 1], g, *parts, offset=0)
+    K.quantize_group(x[:, :, n - 1:], g, *parts, offset=n - 1)
+    torch.cuda.synchronize()
+    for a, b in zip(whole, parts):
+        assert torch.equal(a, b)
+
+
 def test_quantize_group_strided_input_and_decode_append(cuda):
     base = kv_bf16((1, 4, 3, D), seed=7, device=cuda)
     x = base.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)  # [B,H,T,D] view of a [B,T,H,D] buffer
