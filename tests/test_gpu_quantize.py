@@ -283,6 +283,46 @@ def test_dequantize_prod_matches_oracle(cuda, bits):
     assert np.array_equal(u16(out).reshape(300, D), ref)
 
 
+@pytest.mark.parametrize("bits,prod", [(1, False), (2, False), (3, False), (4, False), (1, True), (2, True),
+                                       (3, True)])
+def test_dequantize_arbitrary_rows_match_oracle(cuda, bits, prod):
+    """Arbitrary code and sign bytes with fp16 norms over nine decades (zeros and subnormals
+    included), decoded from a slot offset of a capacity buffer: 3 x 3001 vectors are 563 tiles
+    of 16, several per wave of the matrix-core decoder, the last one ragged."""
+    rng = np.random.default_rng(900 + 10 * bits + prod)
+    B, H, cap, start, T = 1, 3, 3100, 57, 3001
+    lc = layer_codecs(D, bits + 1 if prod else bits, 0, prod, cuda)
+    codec = lc.key if prod else lc.value
+    assert codec.bits == bits
+
+    def norms16():
+        n = (10.0 ** rng.uniform(-6.0, 3.0, (B, H, cap))).astype(np.float16)
+        n.reshape(-1)[rng.integers(0, n.size, 40)] = 0.0
+        return n
+
+    row = K.row_bytes(D, bits)
+    codes_h = rng.integers(0, 256, (B, H, cap, row), dtype=np.uint8)
+    norms_h = norms16()
+    codes, norms = torch.from_numpy(codes_h).to(cuda), torch.from_numpy(norms_h).to(cuda)
+    R, C, _ = _host(codec)
+    sl = slice(start, start + T)
+    if prod:
+        signs_h = rng.integers(0, 256, (B, H, cap, D // 8), dtype=np.uint8)
+        rnorms_h = norms16()
+        out = K.dequantize_prod(codes, norms, torch.from_numpy(signs_h).to(cuda),
+                                torch.from_numpy(rnorms_h).to(cuda), T, codec, lc.qjl, start=start)
+        ref = O.decode_prod(codes_h[:, :, sl].reshape(-1, row), norms_h[:, :, sl].view(np.uint16).reshape(-1),
+                            signs_h[:, :, sl].reshape(-1, D // 8), rnorms_h[:, :, sl].view(np.uint16).reshape(-1),
+                            bits, D, R, C, lc.qjl.cpu().numpy())
+    else:
+        out = K.dequantize_mse(codes, norms, T, codec, start=start)
+        ref = O.decode_mse(codes_h[:, :, sl].reshape(-1, row), norms_h[:, :, sl].view(np.uint16).reshape(-1),
+                           bits, D, R, C)
+    torch.cuda.synchronize()
+    got = u16(out).reshape(-1, D)
+    assert np.array_equal(got, ref), f"{(got != ref).any(axis=1).sum()} of {ref.shape[0]} rows differ"
+
+
 def test_norms_correctly_rounded_over_a_million_vectors(cuda, golden_dir):
     """Stored norms are fp16(correctly rounded sqrt(fma chain)) for 1M vectors; about one in
     4000 lands on an fp16 rounding midpoint, where a square root one ulp low (the bare

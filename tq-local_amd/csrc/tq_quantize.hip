@@ -20,13 +20,13 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "tq_common.h"
 
 namespace {
 
 constexpr int D = TQ_DIM;
-constexpr int QBLOCK = 256;  // lanes (= vectors) per workgroup of the lane-per-vector decoder
 
 struct QuantArgs {
     const uint16_t* x;
@@ -631,79 +631,122 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
     }
 }
 
-// ------------------------------------------------------------------- dequantise
+// ------------------------------------------------------------------- decoders
 // out = bf16((C[code] @ R) * f32(norm)); with QJL (keys of Q_prod) the reference's
 // correction is added in bf16: corr = bf16(((s @ S) * rnorm) * sqrt(pi/2)/D),
 // out = bf16(f32(khat) + f32(corr))   (runtime/packed_qmse_cache.py:312-330, 404-435).
-template <int BITS, bool QJL>
-__global__ __launch_bounds__(QBLOCK) void dequantize_kernel(const uint8_t* __restrict__ codes,
-                                                            const uint16_t* __restrict__ norms,
-                                                            const uint8_t* __restrict__ signs,
-                                                            const uint16_t* __restrict__ rnorms,
-                                                            int64_t tokens, int64_t cap, int64_t n_vec,
-                                                            const float* __restrict__ R,
-                                                            const float* __restrict__ centers,
-                                                            const float* __restrict__ S,
-                                                            uint16_t* __restrict__ out) {
-    __shared__ float s_centers[1 << BITS];
-    if (threadIdx.x < (1 << BITS)) s_centers[threadIdx.x] = centers[threadIdx.x];
-    __syncthreads();
-    const int64_t v = (int64_t)blockIdx.x * QBLOCK + threadIdx.x;
-    if (v >= n_vec) return;
-    const int64_t g = v / tokens, t = v % tokens;
-    const int64_t slot = g * cap + t;
-    constexpr int ROW = D * BITS / 8;
-    const uint8_t* row = codes + slot * ROW;
-    float acc[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
-    for (int j = 0; j < D; ++j) {
-        const int pos = j * BITS;
-        uint32_t pair = row[pos >> 3];
-        if ((pos & 7) + BITS > 8) pair |= (uint32_t)row[(pos >> 3) + 1] << 8;
-        const float cj = s_centers[(pair >> (pos & 7)) & ((1u << BITS) - 1u)];
-        const float* rj = R + j * D;
-#pragma unroll
-        for (int d = 0; d < D; ++d) acc[d] = __builtin_fmaf(cj, rj[d], acc[d]);
+// Output dim d is the fma chain j = 0..127 of C[code_j] * R[j][d] (of sign_j * S[j][d] for
+// the correction), the residual decode's order.  On the matrix cores these are the image
+// products above with A = R^T (S^T): a CONTIG image of the transposed matrix leaves dims
+// [32g, 32g + 32) of vector v in lane 16 g + v, which stores them as 64 contiguous bytes.
+// The B operand is C[code] of index 4s + g; each of a vector's four lanes loads the whole
+// code row and takes its own indices from it.
+
+// CONTIG image of M^T: row r of the image is column r of M, its k-index d is row d of M.
+__device__ __forceinline__ void build_image_transposed(float* img, const float* __restrict__ M) {
+    for (int idx = threadIdx.x; idx < D * D; idx += MQ_THREADS) {
+        const int d = idx / D, r = idx % D;  // consecutive threads read along one row of M
+        const int q = r >> 5, t = (r >> 2) & 7, m = 4 * q + (r & 3);
+        const int s = d >> 2, k = d & 3;
+        img[(t * 8 + (s >> 2)) * 256 + (s & 3) + 4 * ((16 * k + m) ^ k)] = M[idx];
     }
-    const float nf = tq::f16_to_f32(norms[slot]);
-    uint32_t kh[D / 2];  // bf16 pairs
+}
+
+// cv[s] = C[code of index 4s + g] for s = 0..31.  Index 4s + g sits at bit (4s + g) BITS of the
+// code row w, inside the 64-bit window that starts at word 4s BITS / 32 (its field ends within
+// 16 bits of bit 4s BITS); w has one zero word past the row's end.  The word indices are
+// template constants so that the row stays in registers.
+template <int BITS, int... S>
+__device__ __forceinline__ void centers_of(const uint32_t* w, int g, const float* cent, float* cv,
+                                           std::integer_sequence<int, S...>) {
+    constexpr uint32_t MASK = (1u << BITS) - 1u;
+    ((cv[S] = cent[(uint32_t)(((uint64_t)w[(4 * S * BITS) >> 5] | ((uint64_t)w[((4 * S * BITS) >> 5) + 1] << 32)) >>
+                               (((4 * S * BITS) & 31) + g * BITS)) &
+                   MASK]),
+     ...);
+}
+
+template <int BITS, bool QJL>
+__global__ __launch_bounds__(MQ_THREADS) void dequantize_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms, const uint8_t* __restrict__ signs,
+    const uint16_t* __restrict__ rnorms, int64_t tokens, int64_t cap, int64_t n_vec, const float* __restrict__ R,
+    const float* __restrict__ centers, const float* __restrict__ S, uint16_t* __restrict__ out, FastDiv tok_div) {
+    __shared__ float4 s_img[(QJL ? 2 : 1) * D * D / 4];  // R^T image (+ S^T image)
+    __shared__ float s_cent[1 << BITS];
+    float* img = reinterpret_cast<float*>(s_img);
+    build_image_transposed(img, R);
+    if constexpr (QJL) build_image_transposed(img + D * D, S);
+    if (threadIdx.x < (1 << BITS)) s_cent[threadIdx.x] = centers[threadIdx.x];
+    __syncthreads();  // the only barrier: each wave then works on its own tiles
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int v = lane & 15, g = lane >> 4;
+    const float4* a_img = s_img + (lane ^ g);
+    constexpr int ROW = D * BITS / 8;  // code bytes per vector
+    constexpr int RW = ROW / 4;
+    const int64_t n_tiles = (n_vec + 15) / 16;
+
+    for (int64_t tile = (int64_t)blockIdx.x * MQ_WAVES + wave; tile < n_tiles;
+         tile += (int64_t)gridDim.x * MQ_WAVES) {
+        const uint32_t vi = (uint32_t)tile * 16u + (uint32_t)v;  // n_vec < 2^31
+        const bool live = vi < (uint64_t)n_vec;
+        int64_t slot = 0;
+        if (live) {
+            const uint32_t gh = fdiv(vi, tok_div);
+            slot = (int64_t)gh * cap + (vi - gh * (uint32_t)tokens);
+        }
+        // the code row (a lane past the end reads slot 0's, which exists, and stores nothing),
+        // one zero word past its end
+        uint32_t w[RW + 1];
+        {
+            const uint4* c4 = reinterpret_cast<const uint4*>(codes + slot * ROW);
 #pragma unroll
-    for (int i = 0; i < D / 2; ++i)
-        kh[i] = tq::f32_to_bf16(acc[2 * i] * nf) | (tq::f32_to_bf16(acc[2 * i + 1] * nf) << 16);
-#pragma unroll
-    for (int i = 0; i < D / 2; ++i) __asm__("" : "+v"(kh[i]));  // packed here: acc dies before the QJL part
-    if constexpr (QJL) {
-        // the correction in two halves of D/2 dims (each dim's fma chain over i is unchanged):
-        // the packed k^ and one half-width accumulator stay live instead of a full one
-        const uint8_t* srow = signs + slot * (D / 8);
-        const float rn = tq::f16_to_f32(rnorms[slot]);
-        const float qs = 1.2533141373155003f / D;  // sqrt(pi/2)/D rounded to fp32
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            float cacc[D / 2];
-#pragma unroll
-            for (int d = 0; d < D / 2; ++d) cacc[d] = 0.0f;
-            for (int i = 0; i < D; ++i) {
-                const float si = ((srow[i >> 3] >> (i & 7)) & 1u) ? 1.0f : -1.0f;
-                const float* Si = S + i * D + half * (D / 2);
-#pragma unroll
-                for (int d = 0; d < D / 2; ++d) cacc[d] = __builtin_fmaf(si, Si[d], cacc[d]);
+            for (int c = 0; c < BITS; ++c) {
+                const uint4 q = c4[c];
+                w[4 * c] = q.x, w[4 * c + 1] = q.y, w[4 * c + 2] = q.z, w[4 * c + 3] = q.w;
             }
+            w[RW] = 0u;
+        }
+        float cv[32];
+        centers_of<BITS>(w, g, s_cent, cv, std::make_integer_sequence<int, 32>{});
+        f32x4 acc[8];
+        image_products(a_img, cv, acc);
+        const float nf = live ? tq::f16_to_f32(norms[slot]) : 0.0f;
+        uint32_t kh[16];  // bf16 pairs of dims 32g + 2p, 32g + 2p + 1
 #pragma unroll
-            for (int i = 0; i < D / 4; ++i) {
-                const int p = half * (D / 4) + i;
-                const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((cacc[2 * i] * rn) * qs));
-                const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((cacc[2 * i + 1] * rn) * qs));
+        for (int p = 0; p < 16; ++p)
+            kh[p] = tq::f32_to_bf16(acc[p >> 1][2 * (p & 1)] * nf) |
+                    (tq::f32_to_bf16(acc[p >> 1][2 * (p & 1) + 1] * nf) << 16);
+        if constexpr (QJL) {
+            // sign of index 4s + g: word s / 8, bit 4 (s % 8) + g of the 16-byte sign row
+            uint4 sw = make_uint4(0u, 0u, 0u, 0u);
+            float rn = 0.0f;
+            if (live) {
+                sw = reinterpret_cast<const uint4*>(signs + slot * (D / 8))[0];
+                rn = tq::f16_to_f32(rnorms[slot]);
+            }
+            const uint32_t sws[4] = {sw.x, sw.y, sw.z, sw.w};
+            float sv[32];
+#pragma unroll
+            for (int s = 0; s < 32; ++s) sv[s] = ((sws[s >> 3] >> (4 * (s & 7) + g)) & 1u) ? 1.0f : -1.0f;
+            f32x4 pacc[8];
+            image_products(a_img + D * D / 4, sv, pacc);
+            const float qs = 1.2533141373155003f / D;  // sqrt(pi/2)/D rounded to fp32
+#pragma unroll
+            for (int p = 0; p < 16; ++p) {
+                const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1)] * rn) * qs));
+                const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1) + 1] * rn) * qs));
                 const float k0 = tq::bf16_to_f32(kh[p] & 0xFFFFu) + c0;
                 const float k1 = tq::bf16_to_f32(kh[p] >> 16) + c1;
                 kh[p] = tq::f32_to_bf16(k0) | (tq::f32_to_bf16(k1) << 16);
             }
         }
-    }
-    uint4* o4 = reinterpret_cast<uint4*>(out + v * D);
+        if (live) {
+            uint4* o4 = reinterpret_cast<uint4*>(out + (int64_t)vi * D + 32 * g);
 #pragma unroll
-    for (int i = 0; i < D / 8; ++i) o4[i] = make_uint4(kh[4 * i], kh[4 * i + 1], kh[4 * i + 2], kh[4 * i + 3]);
+            for (int i = 0; i < 4; ++i) o4[i] = make_uint4(kh[4 * i], kh[4 * i + 1], kh[4 * i + 2], kh[4 * i + 3]);
+        }
+    }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -717,9 +760,9 @@ int check_common(const uint16_t* x, int batch, int heads, int64_t tokens, int di
     return TQ_OK;
 }
 
-// Workgroups of the matrix-core encoder that fit on the device at once (each loops over
-// tiles, so more would only repeat the LDS image set-up).
-template <int BITS, bool PROD>
+// Workgroups of a matrix-core kernel that fit on the device at once (each loops over tiles,
+// so more would only repeat the LDS image set-up).
+template <auto KERNEL>
 int64_t resident_groups() {
     static int64_t cached[64] = {};
     int dev = 0;
@@ -727,8 +770,7 @@ int64_t resident_groups() {
     if (cached[dev] == 0) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, quantize_mfma_kernel<BITS, PROD>, MQ_THREADS,
-                                                         0) != hipSuccess || per_cu < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, KERNEL, MQ_THREADS, 0) != hipSuccess || per_cu < 1)
             per_cu = 1;
         cached[dev] = (int64_t)cus * per_cu;
     }
@@ -739,7 +781,7 @@ template <int BITS, bool PROD>
 int launch_quantize(const QuantArgs& a, hipStream_t s) {
     if (a.n_vec >= MQ_MIN_VECTORS && a.n_vec < ((int64_t)1 << 31)) {
         const int64_t tiles = (a.n_vec + 15) / 16;
-        const int64_t groups = std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, resident_groups<BITS, PROD>());
+        const int64_t groups = std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, resident_groups<quantize_mfma_kernel<BITS, PROD>>());
         hipLaunchKernelGGL((quantize_mfma_kernel<BITS, PROD>), dim3((unsigned)groups), dim3(MQ_THREADS), 0, s, a.x,
                            a.heads, a.tokens, a.n_vec, a.x_sb, a.x_sh, a.x_st, a.R, a.centers, a.boundaries, a.S,
                            a.codes, a.norms, a.signs, a.rnorms, a.out_cap, a.out_offset,
@@ -801,6 +843,20 @@ extern "C" int tq_quantize_prod(const uint16_t* x, int batch, int heads, int64_t
 
 namespace {
 
+template <int BITS, bool QJL>
+int run_dequantize(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs, const uint16_t* rnorms,
+                   int64_t tokens, int64_t cap, int64_t n_vec, const float* rotation, const float* centers,
+                   const float* qjl, uint16_t* out, hipStream_t s) {
+    const int64_t tiles = (n_vec + 15) / 16;
+    const int64_t wgs =
+        std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, resident_groups<dequantize_kernel<BITS, QJL>>());
+    hipLaunchKernelGGL((dequantize_kernel<BITS, QJL>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes, norms,
+                       signs, rnorms, tokens, cap, n_vec, rotation, centers, qjl, out,
+                       make_fastdiv((uint32_t)tokens));
+    TQ_CHECK_LAUNCH();
+    return TQ_OK;
+}
+
 template <bool QJL>
 int launch_dequantize(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs, const uint16_t* rnorms,
                       int64_t groups, int64_t tokens, int64_t cap, int dim, int bits, const float* rotation,
@@ -809,23 +865,21 @@ int launch_dequantize(const uint8_t* codes, const uint16_t* norms, const uint8_t
         return TQ_ERR_INVALID_ARGUMENT;
     if (QJL && (!signs || !rnorms || !qjl)) return TQ_ERR_INVALID_ARGUMENT;
     if (dim != TQ_DIM) return TQ_ERR_UNSUPPORTED;
-    if (!aligned16(codes) || !aligned16(out)) return TQ_ERR_UNSUPPORTED;
+    if (!aligned16(codes) || !aligned16(out) || (QJL && !aligned16(signs))) return TQ_ERR_UNSUPPORTED;
+    if (bits < 1 || bits > 4) return TQ_ERR_INVALID_ARGUMENT;
     const int64_t n_vec = groups * tokens;
-    const int64_t blocks = (n_vec + QBLOCK - 1) / QBLOCK;
-    if (blocks == 0) return TQ_OK;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n_vec == 0) return TQ_OK;
+    if (n_vec >= ((int64_t)1 << 31)) return TQ_ERR_UNSUPPORTED;
+    auto run = [&](auto b) {
+        return run_dequantize<decltype(b)::value, QJL>(codes, norms, signs, rnorms, tokens, cap, n_vec, rotation,
+                                                        centers, qjl, out, static_cast<hipStream_t>(stream));
+    };
     switch (bits) {
-#define TQ_DQ(B)                                                                                             \
-    case B:                                                                                                  \
-        hipLaunchKernelGGL((dequantize_kernel<B, QJL>), dim3((unsigned)blocks), dim3(QBLOCK), 0, s, codes, norms, \
-                           signs, rnorms, tokens, cap, n_vec, rotation, centers, qjl, out);                    \
-        break;
-        TQ_DQ(1) TQ_DQ(2) TQ_DQ(3) TQ_DQ(4)
-#undef TQ_DQ
-        default: return TQ_ERR_INVALID_ARGUMENT;
+        case 1: return run(std::integral_constant<int, 1>{});
+        case 2: return run(std::integral_constant<int, 2>{});
+        case 3: return run(std::integral_constant<int, 3>{});
+        default: return run(std::integral_constant<int, 4>{});
     }
-    TQ_CHECK_LAUNCH();
-    return TQ_OK;
 }
 
 }  // namespace
