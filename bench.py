@@ -368,6 +368,69 @@ def bench_host(args, dev) -> dict:
             "calls": out}
 
 
+def bench_dequant(args, dev) -> dict:
+    """The decoders (`tq_dequantize_prod` for keys, `tq_dequantize_mse` for values) on
+    `--context` tokens of every (batch row, KV head): a whole C2 layer by default; 1024 tokens is
+    one range of the chunked attention path.  Device time per call (HIP events on the launch
+    stream), and the fp32 matrix work against the MI355X dense fp32 matrix peak."""
+    import torch
+
+    from turboquant.runtime import kernels as K
+    from turboquant.runtime.params import layer_codecs
+
+    B, Hkv, N, D, bits = args.batch, args.kv_heads, args.context, 128, args.bits
+    qjl = not args.no_qjl
+    lc = layer_codecs(D, bits, 0, qjl, dev)
+    gen = torch.Generator(device=dev).manual_seed(5)
+
+    def rand_bytes(*shape):
+        return torch.randint(0, 256, shape, dtype=torch.uint8, device=dev, generator=gen)
+
+    def rand_norms():
+        return torch.rand(B, Hkv, N, device=dev, generator=gen).half()
+
+    kc, kn = rand_bytes(B, Hkv, N, K.row_bytes(D, lc.key_bits)), rand_norms()
+    ks, kr = rand_bytes(B, Hkv, N, D // 8), rand_norms()
+    vc, vn = rand_bytes(B, Hkv, N, K.row_bytes(D, bits)), rand_norms()
+
+    def dec_k():
+        if qjl:
+            K.dequantize_prod(kc, kn, ks, kr, N, lc.key, lc.qjl)
+        else:
+            K.dequantize_mse(kc, kn, N, lc.key)
+
+    def dec_v():
+        K.dequantize_mse(vc, vn, N, lc.value)
+
+    def device_us(fn):
+        for _ in range(max(args.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / args.steps
+
+    n_vec = B * Hkv * N
+    k_us, v_us = device_us(dec_k), device_us(dec_v)
+    # one D x D fp32 matrix-vector product per vector (C[code] @ R), a second one for the QJL correction
+    k_tflops = n_vec * (2 if qjl else 1) * 2 * D * D / (k_us * 1e-6) / 1e12
+    v_tflops = n_vec * 2 * D * D / (v_us * 1e-6) / 1e12
+    peak = 157.3
+    return {"metric": "decode (dequantize) per call", "value": round(k_us + v_us, 2), "unit": "us",
+            "higher_is_better": False, "dtype": "f32",
+            "config": {"workload": f"{N} tokens of B={B} x Hkv={Hkv}: {lc.key_bits}-bit "
+                                   f"{'Q_prod' if qjl else 'Q_mse'} keys, {bits}-bit Q_mse values",
+                       "vectors_per_call": n_vec},
+            "steps": args.steps,
+            "keys": {"us": round(k_us, 2), "tflops": round(k_tflops, 1), "frac": round(k_tflops / peak, 3)},
+            "values": {"us": round(v_us, 2), "tflops": round(v_tflops, 1), "frac": round(v_tflops / peak, 3)},
+            "peak_tflops": peak}
+
+
 def bench_append(args, dev) -> dict:
     """Decode-append: the encoders on one new token per (batch row, KV head), writing in place
     at a slot of a capacity buffer, as a decode step does for every packed layer.  K (Q_prod or
@@ -497,6 +560,8 @@ def main() -> int:
                     help="host cost per decode-attention call (Python wrappers) instead of the C2 line")
     ap.add_argument("--append", action="store_true",
                     help="decode-append encoders (one new token per batch row and KV head) instead of the C2 line")
+    ap.add_argument("--dequant", action="store_true",
+                    help="the decoders on --context tokens per (batch row, KV head) instead of the C2 line")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -517,6 +582,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.append:
         print(json.dumps(bench_append(args, dev)))
+        return 0
+    if args.dequant:
+        print(json.dumps(bench_dequant(args, dev)))
         return 0
     if args.outliers:
         print(json.dumps(bench_split(args, dev)))
