@@ -283,14 +283,18 @@ def test_dequantize_prod_matches_oracle(cuda, bits):
     assert np.array_equal(u16(out).reshape(300, D), ref)
 
 
+@pytest.mark.parametrize("T", [3001, 12001])
 @pytest.mark.parametrize("bits,prod", [(1, False), (2, False), (3, False), (4, False), (1, True), (2, True),
                                        (3, True)])
-def test_dequantize_arbitrary_rows_match_oracle(cuda, bits, prod):
+def test_dequantize_arbitrary_rows_match_oracle(cuda, bits, prod, T):
     """Arbitrary code and sign bytes with fp16 norms over nine decades (zeros and subnormals
-    included), decoded from a slot offset of a capacity buffer: 3 x 3001 vectors are 563 tiles
-    of 16, several per wave of the matrix-core decoder, the last one ragged."""
-    rng = np.random.default_rng(900 + 10 * bits + prod)
-    B, H, cap, start, T = 1, 3, 3100, 57, 3001
+    included), decoded from a slot offset of a capacity buffer.  3 x 3001 vectors are 563 tiles
+    of 16 (each tile's row tiles split over 2 or 4 waves), 3 x 12001 are 2251 (whole tiles per
+    wave, several per wave); the last tile is ragged.  The larger case checks 1500 random rows
+    and the last 40 against the oracle."""
+    rng = np.random.default_rng(900 + 10 * bits + prod + T)
+    B, H, start = 1, 3, 57
+    cap = start + T + 40
     lc = layer_codecs(D, bits + 1 if prod else bits, 0, prod, cuda)
     codec = lc.key if prod else lc.value
     assert codec.bits == bits
@@ -305,21 +309,23 @@ def test_dequantize_arbitrary_rows_match_oracle(cuda, bits, prod):
     norms_h = norms16()
     codes, norms = torch.from_numpy(codes_h).to(cuda), torch.from_numpy(norms_h).to(cuda)
     R, C, _ = _host(codec)
+    n = B * H * T
+    rows = np.arange(n) if T < 5000 else np.union1d(rng.choice(n, 1500, replace=False), np.arange(n - 40, n))
     sl = slice(start, start + T)
+    pick = lambda a: a[:, :, sl].reshape(n, -1)[rows]  # noqa: E731
     if prod:
         signs_h = rng.integers(0, 256, (B, H, cap, D // 8), dtype=np.uint8)
         rnorms_h = norms16()
         out = K.dequantize_prod(codes, norms, torch.from_numpy(signs_h).to(cuda),
                                 torch.from_numpy(rnorms_h).to(cuda), T, codec, lc.qjl, start=start)
-        ref = O.decode_prod(codes_h[:, :, sl].reshape(-1, row), norms_h[:, :, sl].view(np.uint16).reshape(-1),
-                            signs_h[:, :, sl].reshape(-1, D // 8), rnorms_h[:, :, sl].view(np.uint16).reshape(-1),
-                            bits, D, R, C, lc.qjl.cpu().numpy())
+        ref = O.decode_prod(pick(codes_h), pick(norms_h[..., None].view(np.uint16)).reshape(-1), pick(signs_h),
+                            pick(rnorms_h[..., None].view(np.uint16)).reshape(-1), bits, D, R, C,
+                            lc.qjl.cpu().numpy())
     else:
         out = K.dequantize_mse(codes, norms, T, codec, start=start)
-        ref = O.decode_mse(codes_h[:, :, sl].reshape(-1, row), norms_h[:, :, sl].view(np.uint16).reshape(-1),
-                           bits, D, R, C)
+        ref = O.decode_mse(pick(codes_h), pick(norms_h[..., None].view(np.uint16)).reshape(-1), bits, D, R, C)
     torch.cuda.synchronize()
-    got = u16(out).reshape(-1, D)
+    got = u16(out).reshape(-1, D)[rows]
     assert np.array_equal(got, ref), f"{(got != ref).any(axis=1).sum()} of {ref.shape[0]} rows differ"
 
 

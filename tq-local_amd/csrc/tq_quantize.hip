@@ -388,31 +388,33 @@ __device__ __forceinline__ float gram_diag(const f32x4& acc, int v) {
 
 // Rotation / QJL products of one tile: acc[t][i] = chain over d of b[d] * M[row(t, 4g + i)][d],
 // with b held as described above (b[s] = element 4s + g) and `a` this lane's slot of image M.
+// NT < 8 computes the row tiles t = 0..NT-1 of an image pointer advanced by t0 * 8 * 64.
+template <int NT = 8>
 __device__ __forceinline__ void image_products(const float4* __restrict__ a, const float* b, f32x4* acc) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // two register sets of A values: block sb + 1 is read while block sb's products run; the
     // scheduling barriers keep the compiler from hoisting every block's reads to the top
-    float4 cur[8], nxt[8];
+    float4 cur[NT], nxt[NT];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) cur[t] = a[t * 8 * 64];
+    for (int t = 0; t < NT; ++t) cur[t] = a[t * 8 * 64];
 #pragma unroll
     for (int sb = 0; sb < 8; ++sb) {
         if (sb + 1 < 8) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) nxt[t] = a[(t * 8 + sb + 1) * 64];
+            for (int t = 0; t < NT; ++t) nxt[t] = a[(t * 8 + sb + 1) * 64];
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
+            for (int t = 0; t < NT; ++t) {
                 const float ae = e == 0 ? cur[t].x : e == 1 ? cur[t].y : e == 2 ? cur[t].z : cur[t].w;
                 acc[t] = mfma_f32(ae, b[4 * sb + e], acc[t]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) cur[t] = nxt[t];
+        for (int t = 0; t < NT; ++t) cur[t] = nxt[t];
     }
 }
 
@@ -666,7 +668,7 @@ __device__ __forceinline__ void centers_of(const uint32_t* w, int g, const float
      ...);
 }
 
-template <int BITS, bool QJL>
+template <int BITS, bool QJL, int PARTS>
 __global__ __launch_bounds__(MQ_THREADS) void dequantize_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms, const uint8_t* __restrict__ signs,
     const uint16_t* __restrict__ rnorms, int64_t tokens, int64_t cap, int64_t n_vec, const float* __restrict__ R,
@@ -681,13 +683,18 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_kernel(
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int v = lane & 15, g = lane >> 4;
-    const float4* a_img = s_img + (lane ^ g);
+    constexpr int NT = 8 / PARTS;  // row tiles (16 output dims each) per work item
     constexpr int ROW = D * BITS / 8;  // code bytes per vector
     constexpr int RW = ROW / 4;
-    const int64_t n_tiles = (n_vec + 15) / 16;
+    const int64_t n_items = (n_vec + 15) / 16 * PARTS;
 
-    for (int64_t tile = (int64_t)blockIdx.x * MQ_WAVES + wave; tile < n_tiles;
-         tile += (int64_t)gridDim.x * MQ_WAVES) {
+    // work item = (tile of 16 vectors, part): part p computes row tiles [p NT, p NT + NT), the
+    // dims 32g + [4 p NT, 4 p NT + 4 NT) of each of lane 16 g + v's vector
+    for (int64_t item = (int64_t)blockIdx.x * MQ_WAVES + wave; item < n_items;
+         item += (int64_t)gridDim.x * MQ_WAVES) {
+        const int64_t tile = item / PARTS;
+        const int t0 = (int)(item % PARTS) * NT;
+        const float4* a_img = s_img + t0 * 8 * 64 + (lane ^ g);
         const uint32_t vi = (uint32_t)tile * 16u + (uint32_t)v;  // n_vec < 2^31
         const bool live = vi < (uint64_t)n_vec;
         int64_t slot = 0;
@@ -709,12 +716,12 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_kernel(
         }
         float cv[32];
         centers_of<BITS>(w, g, s_cent, cv, std::make_integer_sequence<int, 32>{});
-        f32x4 acc[8];
-        image_products(a_img, cv, acc);
+        f32x4 acc[NT];
+        image_products<NT>(a_img, cv, acc);
         const float nf = live ? tq::f16_to_f32(norms[slot]) : 0.0f;
-        uint32_t kh[16];  // bf16 pairs of dims 32g + 2p, 32g + 2p + 1
+        uint32_t kh[2 * NT];  // bf16 pairs of dims 32g + 4 t0 + 2p, + 2p + 1
 #pragma unroll
-        for (int p = 0; p < 16; ++p)
+        for (int p = 0; p < 2 * NT; ++p)
             kh[p] = tq::f32_to_bf16(acc[p >> 1][2 * (p & 1)] * nf) |
                     (tq::f32_to_bf16(acc[p >> 1][2 * (p & 1) + 1] * nf) << 16);
         if constexpr (QJL) {
@@ -729,11 +736,11 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_kernel(
             float sv[32];
 #pragma unroll
             for (int s = 0; s < 32; ++s) sv[s] = ((sws[s >> 3] >> (4 * (s & 7) + g)) & 1u) ? 1.0f : -1.0f;
-            f32x4 pacc[8];
-            image_products(a_img + D * D / 4, sv, pacc);
+            f32x4 pacc[NT];
+            image_products<NT>(a_img + D * D / 4, sv, pacc);
             const float qs = 1.2533141373155003f / D;  // sqrt(pi/2)/D rounded to fp32
 #pragma unroll
-            for (int p = 0; p < 16; ++p) {
+            for (int p = 0; p < 2 * NT; ++p) {
                 const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1)] * rn) * qs));
                 const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1) + 1] * rn) * qs));
                 const float k0 = tq::bf16_to_f32(kh[p] & 0xFFFFu) + c0;
@@ -742,9 +749,9 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_kernel(
             }
         }
         if (live) {
-            uint4* o4 = reinterpret_cast<uint4*>(out + (int64_t)vi * D + 32 * g);
+            uint4* o4 = reinterpret_cast<uint4*>(out + (int64_t)vi * D + 32 * g + 4 * t0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o4[i] = make_uint4(kh[4 * i], kh[4 * i + 1], kh[4 * i + 2], kh[4 * i + 3]);
+            for (int i = 0; i < NT / 2; ++i) o4[i] = make_uint4(kh[4 * i], kh[4 * i + 1], kh[4 * i + 2], kh[4 * i + 3]);
         }
     }
 }
@@ -843,18 +850,37 @@ extern "C" int tq_quantize_prod(const uint16_t* x, int batch, int heads, int64_t
 
 namespace {
 
+template <int BITS, bool QJL, int PARTS>
+int launch_dequantize_parts(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
+                            const uint16_t* rnorms, int64_t tokens, int64_t cap, int64_t n_vec,
+                            const float* rotation, const float* centers, const float* qjl, uint16_t* out,
+                            hipStream_t s) {
+    const int64_t items = (n_vec + 15) / 16 * PARTS;
+    const int64_t wgs = std::min<int64_t>((items + MQ_WAVES - 1) / MQ_WAVES,
+                                          resident_groups<dequantize_kernel<BITS, QJL, PARTS>>());
+    hipLaunchKernelGGL((dequantize_kernel<BITS, QJL, PARTS>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes,
+                       norms, signs, rnorms, tokens, cap, n_vec, rotation, centers, qjl, out,
+                       make_fastdiv((uint32_t)tokens));
+    TQ_CHECK_LAUNCH();
+    return TQ_OK;
+}
+
+// A call with fewer tiles than the device holds waves splits each tile's row tiles over 2 or 4
+// waves: the same chains, each wave running a half or a quarter of a tile's MFMAs.
 template <int BITS, bool QJL>
 int run_dequantize(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs, const uint16_t* rnorms,
                    int64_t tokens, int64_t cap, int64_t n_vec, const float* rotation, const float* centers,
                    const float* qjl, uint16_t* out, hipStream_t s) {
     const int64_t tiles = (n_vec + 15) / 16;
-    const int64_t wgs =
-        std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, resident_groups<dequantize_kernel<BITS, QJL>>());
-    hipLaunchKernelGGL((dequantize_kernel<BITS, QJL>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes, norms,
-                       signs, rnorms, tokens, cap, n_vec, rotation, centers, qjl, out,
-                       make_fastdiv((uint32_t)tokens));
-    TQ_CHECK_LAUNCH();
-    return TQ_OK;
+    const int64_t waves = resident_groups<dequantize_kernel<BITS, QJL, 1>>() * MQ_WAVES;
+    if (4 * tiles <= waves)
+        return launch_dequantize_parts<BITS, QJL, 4>(codes, norms, signs, rnorms, tokens, cap, n_vec, rotation,
+                                                     centers, qjl, out, s);
+    if (2 * tiles <= waves)
+        return launch_dequantize_parts<BITS, QJL, 2>(codes, norms, signs, rnorms, tokens, cap, n_vec, rotation,
+                                                     centers, qjl, out, s);
+    return launch_dequantize_parts<BITS, QJL, 1>(codes, norms, signs, rnorms, tokens, cap, n_vec, rotation, centers,
+                                                 qjl, out, s);
 }
 
 template <bool QJL>
