@@ -225,7 +225,7 @@ def dequantize_prod(codes: torch.Tensor, norms: torch.Tensor, signs: torch.Tenso
     return out
 
 
-#: attention workspace (call counter, partials, shared q-side tiles) per (device, stream):
+#: attention workspace (the split partials) per (device, stream):
 #: calls on one stream are ordered, so they can share one; calls on two streams get two
 _workspaces: dict[tuple, torch.Tensor] = {}
 #: workspaces replaced by a larger one stay allocated: a HIP graph that captured a call keeps
