@@ -147,6 +147,8 @@ int tq_decode_attention_noalloc(const uint16_t* q, int batch, int q_heads, int k
  * caller).  Replaces reference _decode_group (runtime/packed_qmse_cache.py:404-435)
  * and triton_decode_group (runtime/triton_kernels.py:227-236):
  * out = bf16((C[codes] @ R) * f32(norm)).  rows are `cap` apart per group.
+ * codes and out must be 16-byte aligned, and groups * tokens below 2^31, else
+ * TQ_ERR_UNSUPPORTED.
  */
 int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, int64_t groups, int64_t tokens,
                       int64_t cap, int dim, int bits, const float* rotation, const float* centers,
@@ -156,6 +158,8 @@ int tq_dequantize_mse(const uint8_t* codes, const uint16_t* norms, int64_t group
  * Dequantise packed Q_prod keys to bf16: the Q_mse reconstruction plus the QJL
  * correction, rounded as the reference does (runtime/packed_qmse_cache.py:312-330):
  *   corr = bf16(((signs(+-1) @ S) * rnorm) * sqrt(pi/2)/D);  out = bf16(khat + corr)
+ * codes, signs and out must be 16-byte aligned, and groups * tokens below 2^31,
+ * else TQ_ERR_UNSUPPORTED.
  */
 int tq_dequantize_prod(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
                        const uint16_t* rnorms, int64_t groups, int64_t tokens, int64_t cap, int dim,
