@@ -224,6 +224,50 @@ def _oracle_rows(layer: PackedMSELayer) -> tuple[np.ndarray, np.ndarray]:
     return f(kk), f(vv)
 
 
+@pytest.mark.parametrize("k,bits,extra,qjl,role", [(3, 4, 1, True, "key"), (9, 2, 4, False, "key"),
+                                                   (40, 3, 5, True, "key"), (5, 4, 4, False, "value")])
+def test_dequantize_group_arbitrary_rows_match_oracle(cuda, k, bits, extra, qjl, role):
+    """Arbitrary code and sign bytes with fp16 norms over nine decades (zeros included) for both
+    groups of a split, decoded from a slot offset into one row (normal group merge=0, outlier
+    group merge=1): run-time widths 2..8 and groups of 3..125 channels, 3 x 1001 vectors (188
+    tiles of 16, the last ragged), the decoded range ending at the buffers' last byte."""
+    rng = np.random.default_rng(700 + 10 * k + bits)
+    outl = _channels(k, k)
+    sc = split_codecs(np.setdiff1d(np.arange(D), outl), outl, bits, extra, 0, qjl and role == "key", cuda)
+    groups = (sc.key_normal, sc.key_outlier) if role == "key" else (sc.value_normal, sc.value_outlier)
+    B, H, T, start = 1, 3, 1001, 19
+    cap = start + T
+    out = torch.full((B, H, T, D), 7.0, dtype=torch.bfloat16, device=cuda)
+    ref = np.zeros((B * H * T, D), np.uint16)
+    sl = slice(start, start + T)
+    for gi, g in enumerate(groups):
+        prod = g.qjl_ch is not None
+        rb = K.row_bytes(g.dim, g.bits)
+        codes_h = rng.integers(0, 256, (B, H, cap, rb), dtype=np.uint8)
+        norms_h = (10.0 ** rng.uniform(-6.0, 3.0, (B, H, cap))).astype(np.float16)
+        norms_h.reshape(-1)[rng.integers(0, norms_h.size, 20)] = 0.0
+        extra_args = {}
+        if prod:
+            signs_h = rng.integers(0, 256, (B, H, cap, K.row_bytes(g.dim, 1)), dtype=np.uint8)
+            rnorms_h = (10.0 ** rng.uniform(-6.0, 3.0, (B, H, cap))).astype(np.float16)
+            extra_args = dict(signs=torch.from_numpy(signs_h).to(cuda), rnorms=torch.from_numpy(rnorms_h).to(cuda))
+        K.dequantize_group(torch.from_numpy(codes_h).to(cuda), torch.from_numpy(norms_h).to(cuda), T, g, out,
+                           merge=gi == 1, start=start, **extra_args)
+        R, C, _ = _host(g)
+        hc = codes_h[:, :, sl].reshape(B * H * T, -1)
+        hn = norms_h[:, :, sl].reshape(-1).view(np.uint16)
+        if prod:
+            dec = O.decode_prod(hc, hn, signs_h[:, :, sl].reshape(B * H * T, -1),
+                                rnorms_h[:, :, sl].reshape(-1).view(np.uint16), g.bits, g.dim, R, C,
+                                g.qjl.cpu().numpy())
+        else:
+            dec = O.decode_mse(hc, hn, g.bits, g.dim, R, C)
+        ref[:, g.channels] = dec
+    torch.cuda.synchronize()
+    got = u16(out).reshape(-1, D)
+    assert np.array_equal(got, ref), f"{(got != ref).any(axis=1).sum()} of {ref.shape[0]} rows differ"
+
+
 @pytest.mark.parametrize("qjl,bits,Hq", [(True, 4, 8), (False, 3, 8), (True, 3, 16)])
 def test_split_layer_prefill_append_and_attention(cuda, qjl, bits, Hq):
     """Prefill + lazy decode-append of a split layer: packed groups bit-exact against the

@@ -26,7 +26,10 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 #include "tq_common.h"
+#include "tq_mfma.h"
 
 namespace {
 
@@ -476,6 +479,185 @@ extern "C" int tq_quantize_group(const uint16_t* x, int batch, int heads, int64_
     return TQ_OK;
 }
 
+namespace {
+using namespace tqmx;
+
+// ------------------------------------------------------------------ matrix-core decoder
+// The decoder above on the fp32 matrix cores, as the unsplit decoders: output channel c is the
+// chain j = 0..d-1 of C[code_j] * R[j][c] (of sign_j * S[j][c] for the correction), with R the
+// group's d x D matrix in channel space.  Its image holds R^T behind 128 - d zero k-indices, and
+// the B operand is zero there too, so every chain starts with zero products that leave its +0
+// start unchanged.  Code and sign rows (ceil(d b / 8) and ceil(d / 8) bytes, not aligned) are
+// staged per wave in LDS through range-checked dword buffer loads; lane 16 g + v then takes
+// the fields of indices 4s + g - (128 - d) from row v.  Lane 16 g + v ends with channels
+// [32g, 32g + 32) of vector v and stores them as 64 bytes, the other group's channels zeroed
+// or, with `merge`, kept.
+// Groups of at most this many channels decode one lane per vector (dequantize_group_kernel):
+// its chains are d terms long, where the matrix-core chains are padded to 128 (at a C2 layer
+// the lane kernel is faster below about 24 channels for values, 34 for QJL keys).
+constexpr int GDQ_LANE_MAX_DIM = 24;
+constexpr int GRW = 34;  // staged dwords per code row: up to 128 bytes, a misaligned start, one spare
+constexpr int GSW = 6;   // staged dwords per sign row: up to 16 bytes, a misaligned start, one spare
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t group_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Bits [bit, bit + n) (n <= 8) of the LDS dword array w.
+__device__ __forceinline__ uint32_t staged_bits(const uint32_t* w, uint32_t bit, uint32_t n) {
+    const uint32_t i = bit >> 5;
+    return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[i + 1], w[i], bit & 31), 0, n);
+}
+
+// Row v's bytes [b0, b0 + r) as dwords from the one holding b0 into dst (the four lanes of a
+// vector share the loads); returns b0's bit offset in dst.  `limit` is the buffer's extent in
+// bytes (the descriptor's range): a dword that crosses it is assembled from byte loads, since
+// a dword load past the range reads as zero whole, and bytes past it read as zero.
+__device__ __forceinline__ uint32_t stage_row(uint32_t* dst, __amdgpu_buffer_rsrc_t rs, uint32_t limit, uint32_t b0,
+                                              int r, int nw, int g, bool live) {
+    const uint32_t a0 = b0 & ~3u;
+    const int n = (int)((b0 + (uint32_t)r - a0 + 3) >> 2);
+    for (int i = g; i < nw; i += 4) {
+        const uint32_t off = a0 + 4u * (uint32_t)i;
+        uint32_t w = 0u;
+        if (live && i < n) {
+            if (off + 4u <= limit) {
+                w = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+            } else {
+#pragma unroll
+                for (uint32_t k = 0; k < 4; ++k)
+                    if (off + k < limit) w |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, off + k, 0, 0) << (8 * k);
+            }
+        }
+        dst[i] = w;
+    }
+    return 8 * (b0 - a0);
+}
+
+template <bool QJL>
+__global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms, const uint8_t* __restrict__ signs,
+    const uint16_t* __restrict__ rnorms, int64_t tokens, int64_t cap, int64_t n_vec, uint32_t code_bytes,
+    uint32_t sign_bytes, ChanMask mask, int sub_dim, int bits, const float* __restrict__ R,
+    const float* __restrict__ centers, const float* __restrict__ S, float qs, int merge, uint16_t* __restrict__ out,
+    FastDiv tok_div) {
+    __shared__ float4 s_img[(QJL ? 2 : 1) * D * D / 4];  // R^T image (+ S^T image)
+    __shared__ float s_cent[1 << MAX_BITS];
+    __shared__ uint32_t s_code[MQ_WAVES][16][GRW];
+    __shared__ uint32_t s_sign[QJL ? MQ_WAVES : 1][16][GSW];
+    float* img = reinterpret_cast<float*>(s_img);
+    build_image_transposed(img, R, sub_dim);
+    if constexpr (QJL) build_image_transposed(img + D * D, S, sub_dim);
+    for (int i = threadIdx.x; i < (1 << bits); i += MQ_THREADS) s_cent[i] = centers[i];
+    __syncthreads();  // the only barrier: each wave then works on its own tiles
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int v = lane & 15, g = lane >> 4;
+    const float4* a_img = s_img + (lane ^ g);
+    const int pad = D - sub_dim;
+    const int rb = (sub_dim * bits + 7) >> 3, sbytes = (sub_dim + 7) >> 3;
+    const __amdgpu_buffer_rsrc_t rc = group_rsrc(codes, code_bytes);
+    const __amdgpu_buffer_rsrc_t rsg = group_rsrc(QJL ? signs : codes, QJL ? sign_bytes : 0u);
+    const uint32_t mw = g == 0 ? mask.w[0] : g == 1 ? mask.w[1] : g == 2 ? mask.w[2] : mask.w[3];
+    const int64_t n_tiles = (n_vec + 15) / 16;
+
+    for (int64_t tile = (int64_t)blockIdx.x * MQ_WAVES + wave; tile < n_tiles;
+         tile += (int64_t)gridDim.x * MQ_WAVES) {
+        const uint32_t vi = (uint32_t)tile * 16u + (uint32_t)v;  // n_vec < 2^31
+        const bool live = vi < (uint64_t)n_vec;
+        uint32_t slot = 0;  // slot * row bytes < 2^31 (checked on the host)
+        if (live) {
+            const uint32_t gh = fdiv(vi, tok_div);
+            slot = gh * (uint32_t)cap + (vi - gh * (uint32_t)tokens);
+        }
+        uint32_t* crow = s_code[wave][v];
+        const uint32_t cbit = stage_row(crow, rc, code_bytes, slot * (uint32_t)rb, rb, GRW, g, live);
+        uint32_t* srow = QJL ? s_sign[wave][v] : nullptr;
+        uint32_t sbit = 0;
+        if constexpr (QJL) sbit = stage_row(srow, rsg, sign_bytes, slot * (uint32_t)sbytes, sbytes, GSW, g, live);
+        // the wave's LDS accesses complete in issue order; keep the compiler from moving the
+        // reads above the writes (or the next tile's writes above these reads)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float cv[32];
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            const int j = 4 * s + g - pad;
+            cv[s] = j >= 0 ? s_cent[staged_bits(crow, cbit + (uint32_t)(j * bits), (uint32_t)bits)] : 0.0f;
+        }
+        f32x4 acc[8];
+        image_products(a_img, cv, acc);
+        const float nf = live ? tq::f16_to_f32(norms[slot]) : 0.0f;
+        uint32_t kh[16];  // bf16 pairs of channels 32g + 2p, 32g + 2p + 1
+#pragma unroll
+        for (int p = 0; p < 16; ++p)
+            kh[p] = tq::f32_to_bf16(acc[p >> 1][2 * (p & 1)] * nf) |
+                    (tq::f32_to_bf16(acc[p >> 1][2 * (p & 1) + 1] * nf) << 16);
+        if constexpr (QJL) {
+            float sv[32];
+#pragma unroll
+            for (int s = 0; s < 32; ++s) {
+                const int j = 4 * s + g - pad;
+                sv[s] = j < 0 ? 0.0f : staged_bits(srow, sbit + (uint32_t)j, 1u) ? 1.0f : -1.0f;
+            }
+            f32x4 pacc[8];
+            image_products(a_img + D * D / 4, sv, pacc);
+            const float rn = live ? tq::f16_to_f32(rnorms[slot]) : 0.0f;
+#pragma unroll
+            for (int p = 0; p < 16; ++p) {
+                const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1)] * rn) * qs));
+                const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1) + 1] * rn) * qs));
+                const float k0 = tq::bf16_to_f32(kh[p] & 0xFFFFu) + c0;
+                const float k1 = tq::bf16_to_f32(kh[p] >> 16) + c1;
+                kh[p] = tq::f32_to_bf16(k0) | (tq::f32_to_bf16(k1) << 16);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (live) {
+            uint4* o4 = reinterpret_cast<uint4*>(out + (int64_t)vi * D + 32 * g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t m[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int p = 4 * i + k;
+                    m[k] = (((mw >> (2 * p)) & 1u) ? 0x0000FFFFu : 0u) | (((mw >> (2 * p + 1)) & 1u) ? 0xFFFF0000u : 0u);
+                }
+                uint4 w = make_uint4(kh[4 * i] & m[0], kh[4 * i + 1] & m[1], kh[4 * i + 2] & m[2], kh[4 * i + 3] & m[3]);
+                if (merge) {
+                    const uint4 old = o4[i];
+                    w.x |= old.x & ~m[0];
+                    w.y |= old.y & ~m[1];
+                    w.z |= old.z & ~m[2];
+                    w.w |= old.w & ~m[3];
+                }
+                o4[i] = w;
+            }
+        }
+    }
+}
+
+int64_t group_decoder_groups(bool qjl) {
+    static int64_t cached[2][64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int64_t& c = cached[qjl ? 1 : 0][dev];
+    if (c == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+        const hipError_t e = qjl ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                       &per_cu, dequantize_group_mfma_kernel<true>, MQ_THREADS, 0)
+                                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                       &per_cu, dequantize_group_mfma_kernel<false>, MQ_THREADS, 0);
+        if (e != hipSuccess || per_cu < 1) per_cu = 1;
+        c = (int64_t)cus * per_cu;
+    }
+    return c;
+}
+}  // namespace
+
 extern "C" int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, const uint8_t* signs,
                                    const uint16_t* rnorms, int64_t groups, int64_t tokens, int64_t cap, int dim,
                                    const int32_t* channels, int sub_dim, int bits, const float* rotation,
@@ -491,20 +673,41 @@ extern "C" int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, 
     if (has_qjl && (!signs || !rnorms)) return TQ_ERR_INVALID_ARGUMENT;
     if (!aligned16(out)) return TQ_ERR_UNSUPPORTED;
     const int64_t n_vec = groups * tokens;
-    const int64_t blocks = (n_vec + GBLOCK - 1) / GBLOCK;
-    if (blocks == 0) return TQ_OK;
+    if (n_vec == 0) return TQ_OK;
+    // byte extents from `codes` / `signs` to the last row read: the staging loads are
+    // range-checked against them, and 32-bit row offsets cover them
+    const int64_t last = (groups - 1) * cap + tokens;
+    const int64_t rb = (sub_dim * bits + 7) >> 3, sbytes = (sub_dim + 7) >> 3;
+    if (n_vec >= ((int64_t)1 << 31) || last * rb >= ((int64_t)1 << 31) || cap >= ((int64_t)1 << 31))
+        return TQ_ERR_UNSUPPORTED;
     // sqrt(pi/2)/d in double, rounded once to fp32 (the reference multiplies an fp32
     // tensor by this Python float)
     const float qs = (float)(sqrt(M_PI / 2.0) / (double)sub_dim);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (sub_dim <= GDQ_LANE_MAX_DIM) {
+        const int64_t blocks = (n_vec + GBLOCK - 1) / GBLOCK;
+        if (has_qjl)
+            hipLaunchKernelGGL((dequantize_group_kernel<true>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, codes,
+                               norms, signs, rnorms, tokens, cap, n_vec, mask, sub_dim, bits, rotation, centers, qjl,
+                               qs, merge != 0, out);
+        else
+            hipLaunchKernelGGL((dequantize_group_kernel<false>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, codes,
+                               norms, nullptr, nullptr, tokens, cap, n_vec, mask, sub_dim, bits, rotation, centers,
+                               nullptr, qs, merge != 0, out);
+        TQ_CHECK_LAUNCH();
+        return TQ_OK;
+    }
+    const int64_t tiles = (n_vec + 15) / 16;
+    const int64_t wgs = std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, group_decoder_groups(has_qjl));
+    const FastDiv td = make_fastdiv((uint32_t)tokens);
     if (has_qjl)
-        hipLaunchKernelGGL((dequantize_group_kernel<true>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, codes, norms,
-                           signs, rnorms, tokens, cap, n_vec, mask, sub_dim, bits, rotation, centers, qjl, qs,
-                           merge != 0, out);
+        hipLaunchKernelGGL((dequantize_group_mfma_kernel<true>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes,
+                           norms, signs, rnorms, tokens, cap, n_vec, (uint32_t)(last * rb), (uint32_t)(last * sbytes),
+                           mask, sub_dim, bits, rotation, centers, qjl, qs, merge != 0, out, td);
     else
-        hipLaunchKernelGGL((dequantize_group_kernel<false>), dim3((unsigned)blocks), dim3(GBLOCK), 0, s, codes,
-                           norms, nullptr, nullptr, tokens, cap, n_vec, mask, sub_dim, bits, rotation, centers,
-                           nullptr, qs, merge != 0, out);
+        hipLaunchKernelGGL((dequantize_group_mfma_kernel<false>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes,
+                           norms, nullptr, nullptr, tokens, cap, n_vec, (uint32_t)(last * rb), 0u, mask, sub_dim, bits,
+                           rotation, centers, nullptr, qs, merge != 0, out, td);
     TQ_CHECK_LAUNCH();
     return TQ_OK;
 }

@@ -23,9 +23,11 @@
 #include <utility>
 
 #include "tq_common.h"
+#include "tq_mfma.h"
 
 namespace {
 
+using namespace tqmx;
 constexpr int D = TQ_DIM;
 
 struct QuantArgs {
@@ -272,30 +274,8 @@ __global__ __launch_bounds__(AT) void append_kernel(
 //   STRIDED (Q_prod codes): index 4(4t + i) + q -> lane g holds the indices 4s + g, the
 //           B-operand layout of the residual decode that consumes them; one LDS round trip
 //           regroups them for packing.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-constexpr int MQ_WAVES = 8;                 // waves per workgroup, each on its own tiles
-constexpr int MQ_THREADS = 64 * MQ_WAVES;
 constexpr int64_t MQ_MIN_VECTORS = 4096;    // below this the small-batch encoder is used
 constexpr int LUT_MAX = 512;                // cells of the bucketize grid
-
-__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// floor(n / d) = (n * m) >> s for 0 <= n < 2^31 and 1 <= d < 2^31, with l = ceil(log2 d),
-// s = 31 + l and m = ceil(2^s / d) < 2^32: then 2^s <= m d <= 2^s + 2^l (Granlund and
-// Montgomery, "Division by invariant integers using multiplication", 1994, Theorem 4.2).
-struct FastDiv {
-    uint32_t m, s;
-};
-FastDiv make_fastdiv(uint32_t d) {
-    uint32_t l = 0;
-    while ((1ull << l) < d) ++l;
-    return {(uint32_t)(((1ull << (31 + l)) + d - 1) / d), 31 + l};
-}
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
-    return (uint32_t)(((uint64_t)n * f.m) >> f.s);
-}
 
 // ---- bucketize through a uniform grid
 // code(z) = #{i : b_i < z} for the NB sorted boundaries.  Cells of width w = (smallest gap
@@ -384,38 +364,6 @@ __device__ __forceinline__ float gram_diag(const f32x4& acc, int v) {
     const int r = v & 3;
     const float mine = r == 0 ? acc[0] : r == 1 ? acc[1] : r == 2 ? acc[2] : acc[3];
     return __shfl(mine, v + 16 * (v >> 2));
-}
-
-// Rotation / QJL products of one tile: acc[t][i] = chain over d of b[d] * M[row(t, 4g + i)][d],
-// with b held as described above (b[s] = element 4s + g) and `a` this lane's slot of image M.
-// NT < 8 computes the row tiles t = 0..NT-1 of an image pointer advanced by t0 * 8 * 64.
-template <int NT = 8>
-__device__ __forceinline__ void image_products(const float4* __restrict__ a, const float* b, f32x4* acc) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // two register sets of A values: block sb + 1 is read while block sb's products run; the
-    // scheduling barriers keep the compiler from hoisting every block's reads to the top
-    float4 cur[NT], nxt[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) cur[t] = a[t * 8 * 64];
-#pragma unroll
-    for (int sb = 0; sb < 8; ++sb) {
-        if (sb + 1 < 8) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) nxt[t] = a[(t * 8 + sb + 1) * 64];
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const float ae = e == 0 ? cur[t].x : e == 1 ? cur[t].y : e == 2 ? cur[t].z : cur[t].w;
-                acc[t] = mfma_f32(ae, b[4 * sb + e], acc[t]);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) cur[t] = nxt[t];
-    }
 }
 
 template <int BITS>
@@ -643,16 +591,6 @@ __global__ __launch_bounds__(MQ_THREADS) void quantize_mfma_kernel(
 // [32g, 32g + 32) of vector v in lane 16 g + v, which stores them as 64 contiguous bytes.
 // The B operand is C[code] of index 4s + g; each of a vector's four lanes loads the whole
 // code row and takes its own indices from it.
-
-// CONTIG image of M^T: row r of the image is column r of M, its k-index d is row d of M.
-__device__ __forceinline__ void build_image_transposed(float* img, const float* __restrict__ M) {
-    for (int idx = threadIdx.x; idx < D * D; idx += MQ_THREADS) {
-        const int d = idx / D, r = idx % D;  // consecutive threads read along one row of M
-        const int q = r >> 5, t = (r >> 2) & 7, m = 4 * q + (r & 3);
-        const int s = d >> 2, k = d & 3;
-        img[(t * 8 + (s >> 2)) * 256 + (s & 3) + 4 * ((16 * k + m) ^ k)] = M[idx];
-    }
-}
 
 // cv[s] = C[code of index 4s + g] for s = 0..31.  Index 4s + g sits at bit (4s + g) BITS of the
 // code row w, inside the 64-bit window that starts at word 4s BITS / 32 (its field ends within
