@@ -402,6 +402,36 @@ def bench_dequant(args, dev) -> dict:
     def dec_v():
         K.dequantize_mse(vc, vn, N, lc.value)
 
+    if args.outliers:
+        # outlier-split layers: both channel groups of K and of V into full rows, the first
+        # --outliers channels as the outlier group, one bit wider
+        import numpy as np
+
+        from turboquant.runtime.params import split_codecs
+
+        sc = split_codecs(np.arange(args.outliers, D), np.arange(args.outliers), bits, 1, 0, qjl, dev)
+        out = torch.empty(B, Hkv, N, D, dtype=torch.bfloat16, device=dev)
+
+        def group_data(g):
+            d = [rand_bytes(B, Hkv, N, K.row_bytes(g.dim, g.bits)), rand_norms()]
+            if g.qjl_ch is not None:
+                d += [rand_bytes(B, Hkv, N, K.row_bytes(g.dim, 1)), rand_norms()]
+            return g, d
+
+        kg = [group_data(g) for g in (sc.key_normal, sc.key_outlier)]
+        vg = [group_data(g) for g in (sc.value_normal, sc.value_outlier)]
+
+        def dec_groups(gs):
+            for i, (g, d) in enumerate(gs):
+                extra = {"signs": d[2], "rnorms": d[3]} if len(d) == 4 else {}
+                K.dequantize_group(d[0], d[1], N, g, out, merge=i == 1, **extra)
+
+        def dec_k():  # noqa: F811
+            dec_groups(kg)
+
+        def dec_v():  # noqa: F811
+            dec_groups(vg)
+
     def device_us(fn):
         for _ in range(max(args.warmup, 1)):
             fn()
@@ -423,7 +453,10 @@ def bench_dequant(args, dev) -> dict:
     return {"metric": "decode (dequantize) per call", "value": round(k_us + v_us, 2), "unit": "us",
             "higher_is_better": False, "dtype": "f32",
             "config": {"workload": f"{N} tokens of B={B} x Hkv={Hkv}: {lc.key_bits}-bit "
-                                   f"{'Q_prod' if qjl else 'Q_mse'} keys, {bits}-bit Q_mse values",
+                                   f"{'Q_prod' if qjl else 'Q_mse'} keys, {bits}-bit Q_mse values"
+                                   + (f", outlier split ({args.outliers} channels at {bits + 1} bits; both "
+                                      "groups of K and of V; the flop figures count 128-channel chains)"
+                                      if args.outliers else ""),
                        "vectors_per_call": n_vec},
             "steps": args.steps,
             "keys": {"us": round(k_us, 2), "tflops": round(k_tflops, 1), "frac": round(k_tflops / peak, 3)},

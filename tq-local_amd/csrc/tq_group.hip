@@ -20,6 +20,10 @@
 // therefore bit-identical to the plain encoder / decoder run at D = d on the gathered
 // sub-vectors, which is how the CPU oracle states them.
 //
+// The decoder of groups wider than 24 channels runs on the fp32 matrix cores instead
+// (dequantize_group_mfma_kernel below, with the chains of tq_mfma.h): same chains, same
+// bits.
+//
 // Packed rows are ceil(d*bits/8) code bytes and ceil(d/8) sign bytes per token, LSB
 // first, zero padded (runtime/packed_qmse_cache.py:13-43, 148-154); lanes write them
 // byte by byte, so no alignment is required of those buffers.
