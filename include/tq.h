@@ -202,7 +202,9 @@ int tq_quantize_group(const uint16_t* x, int batch, int heads, int64_t tokens, i
  * aligned): the group's channels get tq_dequantize_mse / tq_dequantize_prod of the
  * sub-vector (QJL correction when qjl is non-NULL, scaled by sqrt(pi/2)/sub_dim); the
  * other channels are zeroed, or kept when `merge` is non-zero.  Decoding the normal
- * group, then the outlier group with merge = 1, gives the full row.
+ * group, then the outlier group with merge = 1, gives the full row.  Code and sign
+ * rows need no alignment; groups * tokens, and the code bytes from `codes` to the last
+ * row decoded, must stay below 2^31, else TQ_ERR_UNSUPPORTED.
  * Replaces reference _decode_merge (runtime/packed_qmse_cache.py:498-515) and
  * _decode_keys_merge_qjl (:456-479), one group per call.
  */
