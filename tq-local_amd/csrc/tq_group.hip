@@ -397,6 +397,7 @@ __global__ __launch_bounds__(GBLOCK) void dequantize_group_kernel(
         for (int k = 0; k < 4; ++k)
             m[k] = (in_group(mask, 8 * i + 2 * k) ? 0x0000FFFFu : 0u) |
                    (in_group(mask, 8 * i + 2 * k + 1) ? 0xFFFF0000u : 0u);
+        if (merge && (m[0] | m[1] | m[2] | m[3]) == 0u) continue;  // no channel of the group: kept as is
         uint4 w = make_uint4(kh[4 * i] & m[0], kh[4 * i + 1] & m[1], kh[4 * i + 2] & m[2], kh[4 * i + 3] & m[3]);
         if (merge) {
             const uint4 old = o4[i];
@@ -629,6 +630,7 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
                     const int p = 4 * i + k;
                     m[k] = (((mw >> (2 * p)) & 1u) ? 0x0000FFFFu : 0u) | (((mw >> (2 * p + 1)) & 1u) ? 0xFFFF0000u : 0u);
                 }
+                if (merge && (m[0] | m[1] | m[2] | m[3]) == 0u) continue;  // no channel of the group
                 uint4 w = make_uint4(kh[4 * i] & m[0], kh[4 * i + 1] & m[1], kh[4 * i + 2] & m[2], kh[4 * i + 3] & m[3]);
                 if (merge) {
                     const uint4 old = o4[i];
