@@ -31,6 +31,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "tq_common.h"
 #include "tq_mfma.h"
@@ -539,7 +540,7 @@ __device__ __forceinline__ uint32_t stage_row(uint32_t* dst, __amdgpu_buffer_rsr
     return 8 * (b0 - a0);
 }
 
-template <bool QJL>
+template <bool QJL, int PARTS>
 __global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms, const uint8_t* __restrict__ signs,
     const uint16_t* __restrict__ rnorms, int64_t tokens, int64_t cap, int64_t n_vec, uint32_t code_bytes,
@@ -564,10 +565,15 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
     const __amdgpu_buffer_rsrc_t rc = group_rsrc(codes, code_bytes);
     const __amdgpu_buffer_rsrc_t rsg = group_rsrc(QJL ? signs : codes, QJL ? sign_bytes : 0u);
     const uint32_t mw = g == 0 ? mask.w[0] : g == 1 ? mask.w[1] : g == 2 ? mask.w[2] : mask.w[3];
-    const int64_t n_tiles = (n_vec + 15) / 16;
+    constexpr int NT = 8 / PARTS;  // row tiles (16 output channels each) per work item
+    const int64_t n_items = (n_vec + 15) / 16 * PARTS;
 
-    for (int64_t tile = (int64_t)blockIdx.x * MQ_WAVES + wave; tile < n_tiles;
-         tile += (int64_t)gridDim.x * MQ_WAVES) {
+    // work item = (tile of 16 vectors, part): part p computes row tiles [p NT, p NT + NT), the
+    // channels 32g + [4 p NT, 4 p NT + 4 NT) of lane 16 g + v's vector
+    for (int64_t item = (int64_t)blockIdx.x * MQ_WAVES + wave; item < n_items;
+         item += (int64_t)gridDim.x * MQ_WAVES) {
+        const int64_t tile = item / PARTS;
+        const int t0 = (int)(item % PARTS) * NT;
         const uint32_t vi = (uint32_t)tile * 16u + (uint32_t)v;  // n_vec < 2^31
         const bool live = vi < (uint64_t)n_vec;
         uint32_t slot = 0;  // slot * row bytes < 2^31 (checked on the host)
@@ -591,12 +597,12 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
             const int j = 4 * s + g - pad;
             cv[s] = j >= 0 ? s_cent[staged_bits(crow, cbit + (uint32_t)(j * bits), (uint32_t)bits)] : 0.0f;
         }
-        f32x4 acc[8];
-        image_products(a_img, cv, acc);
+        f32x4 acc[NT];
+        image_products<NT>(a_img + t0 * 8 * 64, cv, acc);
         const float nf = live ? tq::f16_to_f32(norms[slot]) : 0.0f;
-        uint32_t kh[16];  // bf16 pairs of channels 32g + 2p, 32g + 2p + 1
+        uint32_t kh[2 * NT];  // bf16 pairs of channels 32g + 4 t0 + 2p, + 2p + 1
 #pragma unroll
-        for (int p = 0; p < 16; ++p)
+        for (int p = 0; p < 2 * NT; ++p)
             kh[p] = tq::f32_to_bf16(acc[p >> 1][2 * (p & 1)] * nf) |
                     (tq::f32_to_bf16(acc[p >> 1][2 * (p & 1) + 1] * nf) << 16);
         if constexpr (QJL) {
@@ -606,11 +612,11 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
                 const int j = 4 * s + g - pad;
                 sv[s] = j < 0 ? 0.0f : staged_bits(srow, sbit + (uint32_t)j, 1u) ? 1.0f : -1.0f;
             }
-            f32x4 pacc[8];
-            image_products(a_img + D * D / 4, sv, pacc);
+            f32x4 pacc[NT];
+            image_products<NT>(a_img + D * D / 4 + t0 * 8 * 64, sv, pacc);
             const float rn = live ? tq::f16_to_f32(rnorms[slot]) : 0.0f;
 #pragma unroll
-            for (int p = 0; p < 16; ++p) {
+            for (int p = 0; p < 2 * NT; ++p) {
                 const float c0 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1)] * rn) * qs));
                 const float c1 = tq::bf16_to_f32(tq::f32_to_bf16((pacc[p >> 1][2 * (p & 1) + 1] * rn) * qs));
                 const float k0 = tq::bf16_to_f32(kh[p] & 0xFFFFu) + c0;
@@ -621,13 +627,13 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         if (live) {
-            uint4* o4 = reinterpret_cast<uint4*>(out + (int64_t)vi * D + 32 * g);
+            uint4* o4 = reinterpret_cast<uint4*>(out + (int64_t)vi * D + 32 * g + 4 * t0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NT / 2; ++i) {
                 uint32_t m[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const int p = 4 * i + k;
+                    const int p = 2 * t0 + 4 * i + k;  // channel pair of the lane's 32 channels
                     m[k] = (((mw >> (2 * p)) & 1u) ? 0x0000FFFFu : 0u) | (((mw >> (2 * p + 1)) & 1u) ? 0xFFFF0000u : 0u);
                 }
                 if (merge && (m[0] | m[1] | m[2] | m[3]) == 0u) continue;  // no channel of the group
@@ -654,9 +660,9 @@ int64_t group_decoder_groups(bool qjl) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
         const hipError_t e = qjl ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                       &per_cu, dequantize_group_mfma_kernel<true>, MQ_THREADS, 0)
+                                       &per_cu, dequantize_group_mfma_kernel<true, 1>, MQ_THREADS, 0)
                                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                       &per_cu, dequantize_group_mfma_kernel<false>, MQ_THREADS, 0);
+                                       &per_cu, dequantize_group_mfma_kernel<false, 1>, MQ_THREADS, 0);
         if (e != hipSuccess || per_cu < 1) per_cu = 1;
         c = (int64_t)cus * per_cu;
     }
@@ -703,17 +709,35 @@ extern "C" int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, 
         TQ_CHECK_LAUNCH();
         return TQ_OK;
     }
+    // a call with fewer tiles than the device holds waves splits each tile's row tiles over
+    // 2 or 4 waves (the same chains)
     const int64_t tiles = (n_vec + 15) / 16;
-    const int64_t wgs = std::min<int64_t>((tiles + MQ_WAVES - 1) / MQ_WAVES, group_decoder_groups(has_qjl));
+    const int64_t resident = group_decoder_groups(has_qjl);
+    const int parts = 4 * tiles <= resident * MQ_WAVES ? 4 : 2 * tiles <= resident * MQ_WAVES ? 2 : 1;
+    const int64_t wgs = std::min<int64_t>((tiles * parts + MQ_WAVES - 1) / MQ_WAVES, resident);
     const FastDiv td = make_fastdiv((uint32_t)tokens);
-    if (has_qjl)
-        hipLaunchKernelGGL((dequantize_group_mfma_kernel<true>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes,
-                           norms, signs, rnorms, tokens, cap, n_vec, (uint32_t)(last * rb), (uint32_t)(last * sbytes),
-                           mask, sub_dim, bits, rotation, centers, qjl, qs, merge != 0, out, td);
-    else
-        hipLaunchKernelGGL((dequantize_group_mfma_kernel<false>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes,
-                           norms, nullptr, nullptr, tokens, cap, n_vec, (uint32_t)(last * rb), 0u, mask, sub_dim, bits,
-                           rotation, centers, nullptr, qs, merge != 0, out, td);
+    const uint32_t cbytes = (uint32_t)(last * rb), sgbytes = has_qjl ? (uint32_t)(last * sbytes) : 0u;
+    auto launch = [&](auto qjl_c, auto parts_c) {
+        constexpr bool Q = decltype(qjl_c)::value;
+        constexpr int PP = decltype(parts_c)::value;
+        hipLaunchKernelGGL((dequantize_group_mfma_kernel<Q, PP>), dim3((unsigned)wgs), dim3(MQ_THREADS), 0, s, codes,
+                           norms, Q ? signs : nullptr, Q ? rnorms : nullptr, tokens, cap, n_vec, cbytes, sgbytes, mask,
+                           sub_dim, bits, rotation, centers, Q ? qjl : nullptr, qs, merge != 0, out, td);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P4 = std::integral_constant<int, 4>;
+    if (has_qjl) {
+        if (parts == 4) launch(T{}, P4{});
+        else if (parts == 2) launch(T{}, P2{});
+        else launch(T{}, P1{});
+    } else {
+        if (parts == 4) launch(F{}, P4{});
+        else if (parts == 2) launch(F{}, P2{});
+        else launch(F{}, P1{});
+    }
     TQ_CHECK_LAUNCH();
     return TQ_OK;
 }
