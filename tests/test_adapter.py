@@ -173,6 +173,12 @@ def test_session_settings_and_bit_checks():
     assert s.compatibility_report()["compatible"] and s.last_telemetry() is None
     with pytest.raises(ValueError, match="unsupported"):
         TurboQuantSession(model=model, tokenizer=CharTokenizer(), bits=1, use_qjl_keys=True)
+    # settings are plain attributes, as the reference's: an assignment reaches the next generate
+    s.bits, s.use_qjl_keys = 4, True
+    assert (s.codec.bits, s.codec.use_qjl_keys, s.codec.mode()) == (4, True, "Q_prod")
+    s.bits = 9
+    with pytest.raises(ValueError, match="unsupported"):
+        s.generate(prompt="ab", max_new_tokens=1)
     with pytest.raises(ValueError, match="out of range"):
         turboquant.activate(model, CharTokenizer(), bits=4, num_outlier_channels=4, outlier_extra_bits=5, quiet=True)
     assert not turboquant.is_active(model)

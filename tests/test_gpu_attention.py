@@ -137,6 +137,22 @@ def test_attention_full_length_c2_rows(cuda):
     check(out32, O.fused_attention_f64(u16(q), host_layer(lc, L, N)))
 
 
+def test_attention_c2_geometry(cuda):
+    """BASELINE config 2 exactly as the bench launches it: B=8, Hq=32, Hkv=8, N=32768, 4-bit
+    Q_prod keys / 4-bit Q_mse values, so the kernel runs its 64-group x 4-split grid of
+    8192-token workgroups.  Batch rows 0 and 7 against the fp64 oracle (2e-3 of |out| on the
+    fp32 output); the bf16 output of every row is the RNE rounding of the fp32 output."""
+    B, Hq, Hkv, N = 8, 32, 8, 32768
+    lc, L = build_layer(cuda, B, Hkv, N, 4, True, seed=808)
+    q = query_bf16(B, Hq, D, seed=808, device=cuda)
+    out16, out32 = run(lc, L, q, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(u16(out16), O.f32_to_bf16_bits(out32.cpu().numpy()))
+    for b in (0, B - 1):
+        row = host_layer(lc, {k: (None if v is None else v[b:b + 1]) for k, v in L.items()}, N)
+        check(out32[b:b + 1], O.fused_attention_f64(u16(q[b:b + 1]), row))
+
+
 def test_attention_full_size_c3(cuda):
     """BASELINE config 3 at its full shape (B=16, Hq=32, Hkv=8, N=65536, 3-bit Q_mse keys and
     values, codes straddling bytes and words): rows 0 and 15 against the fp64 oracle."""
@@ -203,3 +219,18 @@ def test_graph_replay_matches_eager(cuda):
             assert torch.equal(o, e)
         run(*lcs[0], qs[0], ns[0])  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_query_at_unaligned_offset(cuda):
+    """A contiguous bf16 query view at a storage offset that is not 16-byte aligned (the
+    kernels read q 16 bytes at a time) gives the aligned query's output."""
+    lc, L = build_layer(cuda, 2, 2, 300, 4, True, seed=12)
+    q = query_bf16(2, 8, D, seed=12, device=cuda)
+    base = torch.empty(q.numel() + 1, dtype=torch.bfloat16, device=cuda)
+    qv = base[1:].view(2, 8, D)
+    qv.copy_(q)
+    assert qv.data_ptr() % 16 != 0 and qv.is_contiguous()
+    _, want = run(lc, L, q, 300)
+    _, got = run(lc, L, qv, 300)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

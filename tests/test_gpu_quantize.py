@@ -221,11 +221,12 @@ def test_small_batch_and_matrix_core_encoders_agree(cuda, bits, prod):
         assert torch.equal(a, b)
 
 
-def test_quantize_full_size_c2_subsample(cuda):
-    """BASELINE config 2 key layer (B=8, Hkv=8, N=32768, 4-bit Q_prod): a random
-    2048-vector subsample is bit-exact against the oracle; the whole layer
-    satisfies the size-independent invariants (codes decode to unit-norm-ish
-    directions, norms equal |x| to fp16 rounding)."""
+def test_quantize_full_size_c2_key_layer(cuda):
+    """BASELINE config 2 key layer (B=8, Hkv=8, N=32768, 4-bit Q_prod: 3-bit codes + QJL):
+    all 2,097,152 vectors' codes, norms, sign bits and residual norms bit-exact against the
+    oracle (run on the host's cores in chunks: the oracle's C calls release the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+
     B, H, N = 8, 8, 32768
     x = kv_bf16((B, H, N, D), seed=2024, device=cuda)
     lc = layer_codecs(D, 4, 0, True, cuda)
@@ -235,18 +236,22 @@ def test_quantize_full_size_c2_subsample(cuda):
     rnorms = torch.empty(B, H, N, dtype=torch.float16, device=cuda)
     K.quantize_prod(x, lc.key, lc.qjl, codes, norms, signs, rnorms)
     torch.cuda.synchronize()
-    # invariant: stored norm == fp16(|x|) up to the fp32 summation order (<= 1 fp16 ulp)
-    ref_norm = x.float().norm(dim=-1)
-    rel = ((norms.float() - ref_norm).abs() / ref_norm).max().item()
-    assert rel < 1e-3
-    idx = torch.randperm(B * H * N, generator=torch.Generator().manual_seed(5))[:2048]
-    xs = u16(x).reshape(-1, D)[idx.numpy()]
+    xs = u16(x).reshape(-1, D)
+    del x
     R, C, bnd = _host(lc.key)
-    rc, rn, rs, rr = O.encode_prod(xs, 3, R, C, bnd, lc.qjl.cpu().numpy())
-    assert np.array_equal(codes.view(-1, 48)[idx.to(cuda)].cpu().numpy(), rc)
-    assert np.array_equal(u16(norms).reshape(-1)[idx.numpy()], rn)
-    assert np.array_equal(signs.view(-1, 16)[idx.to(cuda)].cpu().numpy(), rs)
-    assert np.array_equal(u16(rnorms).reshape(-1)[idx.numpy()], rr)
+    S = lc.qjl.cpu().numpy()
+    got = (codes.view(-1, 48).cpu().numpy(), u16(norms).reshape(-1), signs.view(-1, 16).cpu().numpy(),
+           u16(rnorms).reshape(-1))
+    chunk = 1 << 15
+    starts = range(0, xs.shape[0], chunk)
+
+    def one(s):
+        ref = O.encode_prod(xs[s:s + chunk], 3, R, C, bnd, S)
+        return [int((g[s:s + chunk] != r).sum()) for g, r in zip(got, ref)]
+
+    with ThreadPoolExecutor(max_workers=min(16, O.cpu_count())) as pool:
+        bad = np.array(list(pool.map(one, starts))).sum(axis=0)
+    assert bad.tolist() == [0, 0, 0, 0], f"differing code bytes / norms / sign bytes / rnorms: {bad.tolist()}"
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])

@@ -224,18 +224,23 @@ def _oracle_rows(layer: PackedMSELayer) -> tuple[np.ndarray, np.ndarray]:
     return f(kk), f(vv)
 
 
+@pytest.mark.parametrize("T", [1001, 3001, 12001])
 @pytest.mark.parametrize("k,bits,extra,qjl,role", [(3, 4, 1, True, "key"), (9, 2, 4, False, "key"),
-                                                   (40, 3, 5, True, "key"), (5, 4, 4, False, "value")])
-def test_dequantize_group_arbitrary_rows_match_oracle(cuda, k, bits, extra, qjl, role):
+                                                   (40, 3, 5, True, "key"), (5, 4, 4, False, "value"),
+                                                   (40, 4, 2, False, "value")])
+def test_dequantize_group_arbitrary_rows_match_oracle(cuda, k, bits, extra, qjl, role, T):
     """Arbitrary code and sign bytes with fp16 norms over nine decades (zeros included) for both
     groups of a split, decoded from a slot offset into one row (normal group merge=0, outlier
-    group merge=1): run-time widths 2..8 and groups of 3..125 channels, 3 x 1001 vectors (188
-    tiles of 16, the last ragged), the decoded range ending at the buffers' last byte."""
-    rng = np.random.default_rng(700 + 10 * k + bits)
+    group merge=1): run-time widths 2..8 and groups of 3..125 channels, the decoded range ending
+    at the buffers' last byte.  3 x T vectors are 188 / 563 / 2251 tiles of 16 (the last ragged):
+    on a 256-CU GPU the matrix-core decoder of groups wider than 24 channels then splits a tile's
+    row tiles over 4 waves, over 2, or runs whole tiles per wave, so every variant is checked
+    on a QJL key group and a value group of 40 outlier channels."""
+    rng = np.random.default_rng(700 + 10 * k + bits + T)
     outl = _channels(k, k)
     sc = split_codecs(np.setdiff1d(np.arange(D), outl), outl, bits, extra, 0, qjl and role == "key", cuda)
     groups = (sc.key_normal, sc.key_outlier) if role == "key" else (sc.value_normal, sc.value_outlier)
-    B, H, T, start = 1, 3, 1001, 19
+    B, H, start = 1, 3, 19
     cap = start + T
     out = torch.full((B, H, T, D), 7.0, dtype=torch.bfloat16, device=cuda)
     ref = np.zeros((B * H * T, D), np.uint16)

@@ -1181,29 +1181,26 @@ struct SplitArgs {
 };
 
 int cu_count() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess) return 256;
-        hipDeviceProp_t p;
-        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return 256;
-        cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
-    }
-    return cus;
+    static std::atomic<int64_t> cached[tq::MAX_DEVICES];
+    return (int)tq::once_per_device(cached, 256, [](int dev) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        return (int64_t)cus;
+    });
 }
 
 template <int KB, int VB, bool QJL, int GC>
 int wgs_per_cu() {
-    static int occ = 0;
-    if (occ == 0) {
+    static std::atomic<int64_t> cached[tq::MAX_DEVICES];
+    return (int)tq::once_per_device(cached, 1, [](int) {
         int o = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, Cfg<VB, GC, QJL>::NT, 0) !=
                 hipSuccess ||
             o < 1)
             o = 1;
-        occ = o;
-    }
-    return occ;
+        return (int64_t)o;
+    });
 }
 
 int choose_split(int groups, int64_t n_tokens, int target_wgs, int nw, int64_t* tokens_per_split) {

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/tq.h"
 
 #define TQ_DIM 128          // head_dim supported by the kernels
@@ -48,6 +50,22 @@ __device__ __forceinline__ uint32_t extract_bits(const uint32_t* w, int pos) {
     const int wi = pos >> 5, sh = pos & 31;
     if (sh + N > 32) return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh), 0, N);
     return __builtin_amdgcn_ubfe(w[wi], sh, N);
+}
+
+// Host: a per-device figure (CU count, occupancy) computed on the first call for the current
+// device and kept.  Host threads racing on a first call compute the same value and publish it
+// with an atomic store, so there is no data race; `slots` is a zero-initialised static array.
+constexpr int MAX_DEVICES = 64;
+template <typename F>
+inline int64_t once_per_device(std::atomic<int64_t>* slots, int64_t fallback, F&& compute) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return fallback;
+    int64_t v = slots[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        v = compute(dev);
+        slots[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
 }
 
 }  // namespace tq

@@ -652,11 +652,8 @@ __global__ __launch_bounds__(MQ_THREADS) void dequantize_group_mfma_kernel(
 }
 
 int64_t group_decoder_groups(bool qjl) {
-    static int64_t cached[2][64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int64_t& c = cached[qjl ? 1 : 0][dev];
-    if (c == 0) {
+    static std::atomic<int64_t> cached[2][tq::MAX_DEVICES];
+    return tq::once_per_device(cached[qjl ? 1 : 0], 256, [qjl](int dev) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
         const hipError_t e = qjl ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -664,9 +661,8 @@ int64_t group_decoder_groups(bool qjl) {
                                  : hipOccupancyMaxActiveBlocksPerMultiprocessor(
                                        &per_cu, dequantize_group_mfma_kernel<false, 1>, MQ_THREADS, 0);
         if (e != hipSuccess || per_cu < 1) per_cu = 1;
-        c = (int64_t)cus * per_cu;
-    }
-    return c;
+        return (int64_t)cus * per_cu;
+    });
 }
 }  // namespace
 

@@ -709,17 +709,14 @@ int check_common(const uint16_t* x, int batch, int heads, int64_t tokens, int di
 // so more would only repeat the LDS image set-up).
 template <auto KERNEL>
 int64_t resident_groups() {
-    static int64_t cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
+    static std::atomic<int64_t> cached[tq::MAX_DEVICES];
+    return tq::once_per_device(cached, 256, [](int dev) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, KERNEL, MQ_THREADS, 0) != hipSuccess || per_cu < 1)
             per_cu = 1;
-        cached[dev] = (int64_t)cus * per_cu;
-    }
-    return cached[dev];
+        return (int64_t)cus * per_cu;
+    });
 }
 
 template <int BITS, bool PROD>

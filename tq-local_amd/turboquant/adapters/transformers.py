@@ -232,18 +232,22 @@ class TurboQuantSession:
         self.tokenizer = tokenizer
         self.variant = variant
         self.compatibility = report
-        self.codec = _Codec(bits, rotation_seed, num_outlier_channels, outlier_extra_bits, use_qjl_keys,
-                            quantize_decode, norm_guard).check()
+        # plain attributes, as the reference's (assigning one changes the next generate)
+        self.bits = bits
+        self.rotation_seed = rotation_seed
+        self.num_outlier_channels = num_outlier_channels
+        self.outlier_extra_bits = outlier_extra_bits
+        self.use_qjl_keys = use_qjl_keys
+        self.quantize_decode = quantize_decode
+        self.norm_guard = norm_guard
+        self.codec.check()
         self._last_output: GenerationOutput | None = None
 
-    # the reference exposes the settings as plain attributes
-    bits = property(lambda self: self.codec.bits)
-    rotation_seed = property(lambda self: self.codec.rotation_seed)
-    num_outlier_channels = property(lambda self: self.codec.num_outlier_channels)
-    outlier_extra_bits = property(lambda self: self.codec.outlier_extra_bits)
-    use_qjl_keys = property(lambda self: self.codec.use_qjl_keys)
-    quantize_decode = property(lambda self: self.codec.quantize_decode)
-    norm_guard = property(lambda self: self.codec.norm_guard)
+    @property
+    def codec(self) -> _Codec:
+        """The settings as they stand now (built on every read, so assignments take effect)."""
+        return _Codec(self.bits, self.rotation_seed, self.num_outlier_channels, self.outlier_extra_bits,
+                      self.use_qjl_keys, self.quantize_decode, self.norm_guard)
 
     @classmethod
     def from_pretrained(cls, model_id_or_path: str, *, revision=None, dtype="auto", device_map="auto",
@@ -264,7 +268,7 @@ class TurboQuantSession:
         encoded = _encode_prompt(self.tokenizer, prompt, messages, add_generation_prompt)
         device = next(self.model.parameters()).device
         inputs = {name: t.to(device) for name, t in encoded.items()}
-        self._last_output = self.codec.run(self.model, self.tokenizer, inputs, max_new_tokens, self.variant)
+        self._last_output = self.codec.check().run(self.model, self.tokenizer, inputs, max_new_tokens, self.variant)
         return self._last_output if return_output else self._last_output.text
 
     def last_metrics(self) -> dict[str, Any] | None:

@@ -25,6 +25,7 @@ rotated space; the reference's fused kernel refuses such layers
 from __future__ import annotations
 
 import math
+import threading
 from typing import TYPE_CHECKING
 
 import torch
@@ -52,10 +53,10 @@ def _attend_mask(attention_mask: torch.Tensor, B: int, total: int) -> torch.Tens
     return m
 
 
-#: the ranges of the last mask seen (an HF forward hands every layer the same mask tensor):
-#: (mask, its version counter, B, total, check) -> (starts, ends); holding the mask keeps its
-#: memory from being reused by another tensor while the entry is live
-_last_range: tuple | None = None
+#: the ranges of the last mask seen, per host thread (an HF forward hands every layer the same
+#: mask tensor): (mask, its version counter, B, total, check) -> (starts, ends); holding the mask
+#: keeps its memory from being reused by another tensor while the entry is live
+_tls = threading.local()
 
 
 def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device, check_contiguous: bool = True):
@@ -68,10 +69,9 @@ def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device
     callers that know the mask's shape pass False.  The result for one mask tensor is
     computed once and reused by the following layers of the same forward.
     """
-    global _last_range
     if attention_mask is None:
         return None, None
-    c = _last_range
+    c = getattr(_tls, "last_range", None)
     if (c is not None and c[0] is attention_mask and c[1] == attention_mask._version
             and c[2:6] == (B, total, check_contiguous, device)):
         if c[6] is None:
@@ -80,9 +80,9 @@ def _valid_range(attention_mask: torch.Tensor | None, B: int, total: int, device
     try:
         result = _compute_range(attention_mask, B, total, device, check_contiguous)
     except _HoleyMask:
-        _last_range = (attention_mask, attention_mask._version, B, total, check_contiguous, device, None)
+        _tls.last_range = (attention_mask, attention_mask._version, B, total, check_contiguous, device, None)
         raise
-    _last_range = (attention_mask, attention_mask._version, B, total, check_contiguous, device, result)
+    _tls.last_range = (attention_mask, attention_mask._version, B, total, check_contiguous, device, result)
     return result
 
 

@@ -286,8 +286,8 @@ def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.T
         q = q[:, :, 0, :]
     if q.dtype != torch.bfloat16:
         q = q.to(torch.bfloat16)
-    if not q.is_contiguous():
-        q = q.contiguous()
+    if not q.is_contiguous() or q.data_ptr() % 16:
+        q = q.contiguous() if q.data_ptr() % 16 == 0 else q.clone(memory_format=torch.contiguous_format)
     if not (q.is_cuda and k_codes.is_cuda and v_codes.is_cuda):
         _require_gpu(q, k_codes, v_codes)
     B, Hq, D = q.shape
@@ -334,6 +334,8 @@ def decode_attention_groups(q: torch.Tensor, groups: list[dict], *, n_tokens: in
             raise ValueError("decode_attention_groups takes exactly one query token per sequence")
         q = q[:, :, 0, :]
     q = q.to(torch.bfloat16).contiguous()
+    if q.data_ptr() % 16:  # a view at an odd storage offset: the kernels read q 16 bytes at a time
+        q = q.clone()
     first = groups[0]
     _require_gpu(q, first["k_codes"], first["v_codes"], key_stack, value_stack)
     B, Hq, D = q.shape

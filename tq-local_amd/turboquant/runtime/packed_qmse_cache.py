@@ -61,6 +61,16 @@ class PackedTensorMSE:
         return int(self.packed_indices.numel() * self.packed_indices.element_size()
                    + self.norms.numel() * self.norms.element_size())
 
+    def append(self, other: "PackedTensorMSE") -> "PackedTensorMSE":
+        """A new container holding this one's tokens followed by ``other``'s (reference :81-92).
+        The cache layer itself never calls this: it writes new tokens into capacity slots."""
+        if self.original_shape[:2] != other.original_shape[:2] or self.dimension != other.dimension:
+            raise ValueError("Packed tensor append requires matching batch, head, and dimension shape.")
+        b, h, n, d = self.original_shape
+        return PackedTensorMSE(torch.cat((self.packed_indices, other.packed_indices), dim=2).contiguous(),
+                               torch.cat((self.norms, other.norms), dim=2).contiguous(),
+                               (b, h, n + other.original_shape[2], d), self.original_dtype, self.bits)
+
 
 @dataclass
 class PackedQJL:
@@ -73,6 +83,27 @@ class PackedQJL:
     def storage_bytes(self) -> int:
         return int(self.packed_signs.numel() * self.packed_signs.element_size()
                    + self.residual_norms.numel() * self.residual_norms.element_size())
+
+    def append(self, other: "PackedQJL") -> "PackedQJL":
+        """A new sketch holding this one's tokens followed by ``other``'s (reference :135-140)."""
+        return PackedQJL(torch.cat((self.packed_signs, other.packed_signs), dim=2).contiguous(),
+                         torch.cat((self.residual_norms, other.residual_norms), dim=2).contiguous(),
+                         self.dimension)
+
+
+def _codec_of(rotation: torch.Tensor, centers: torch.Tensor | None, boundaries: torch.Tensor | None,
+              bits: int) -> K.CodecParams:
+    """libtq codec from the reference's parameter tensors (fp32, contiguous, on the device).
+    Copies made here are freed after the launch; the caching allocator hands their blocks
+    only to work ordered after the kernel on the same stream."""
+    f32 = lambda t: None if t is None else (t if t.dtype == torch.float32 and t.is_contiguous()  # noqa: E731
+                                            else t.float().contiguous())
+    return K.CodecParams(bits=int(bits), rotation=f32(rotation), centers=f32(centers), boundaries=f32(boundaries))
+
+
+def _packed_rows(t: torch.Tensor) -> torch.Tensor:
+    """A packed [B, H, N, ...] tensor as libtq reads it (groups N slots apart)."""
+    return t if t.is_contiguous() else t.contiguous()
 
 
 def detect_outlier_channels(key_states: torch.Tensor, value_states: torch.Tensor,
@@ -330,6 +361,58 @@ class PackedMSELayer(CacheLayerMixin):
         if self._split is None:
             return None
         return self._qjl("kso", "kro", self._split.key_outlier.dim)
+
+    # --------------------------------------- reference-named kernel boundary
+    # The reference's quantizer boundary (runtime/packed_qmse_cache.py:285-330, 376-435), with
+    # its signatures and return types, each one libtq launch on the current stream.  Inputs
+    # must be on the GPU with head_dim 128 (there is no CPU path); the decoders return bf16
+    # rows (bf16((C[idx] R) n), plus the bf16 QJL correction for keys) cast to the packed
+    # tensor's original dtype, which is the reference's result for bf16 models.
+    @staticmethod
+    def _encode_group(tensor: torch.Tensor, rotation: torch.Tensor, centers: torch.Tensor,
+                      boundaries: torch.Tensor, bits: int) -> PackedTensorMSE:
+        """Q_mse encoder: norms, rotation, bucketize and bit packing (reference :376-402)."""
+        B, H, N, D = (int(v) for v in tensor.shape)
+        codes = torch.empty(B, H, N, K.row_bytes(D, bits), dtype=torch.uint8, device=tensor.device)
+        norms = torch.empty(B, H, N, dtype=torch.float16, device=tensor.device)
+        K.quantize_mse(tensor, _codec_of(rotation, centers, boundaries, bits), codes, norms)
+        return PackedTensorMSE(codes, norms, (B, H, N, D), tensor.dtype, int(bits))
+
+    @staticmethod
+    def _decode_group(packed: PackedTensorMSE, rotation: torch.Tensor, centers: torch.Tensor) -> torch.Tensor:
+        """Q_mse decoder: (C[idx] @ R) * norm (reference :404-435)."""
+        B, H, N, D = packed.original_shape
+        out = K.dequantize_mse(_packed_rows(packed.packed_indices), _packed_rows(packed.norms), N,
+                               _codec_of(rotation, centers, None, packed.bits), dim=D)
+        return out.to(packed.original_dtype)
+
+    def _encode_keys_qjl_group(self, key_states: torch.Tensor, rotation: torch.Tensor, centers: torch.Tensor,
+                               boundaries: torch.Tensor, bits: int,
+                               qjl_matrix: torch.Tensor) -> tuple[PackedTensorMSE, PackedQJL]:
+        """Q_prod key encoder: (bits)-bit Q_mse codes plus the QJL sign sketch of the residual
+        (reference :285-310)."""
+        B, H, N, D = (int(v) for v in key_states.shape)
+        dev = key_states.device
+        codes = torch.empty(B, H, N, K.row_bytes(D, bits), dtype=torch.uint8, device=dev)
+        norms = torch.empty(B, H, N, dtype=torch.float16, device=dev)
+        signs = torch.empty(B, H, N, K.row_bytes(D, 1), dtype=torch.uint8, device=dev)
+        rnorms = torch.empty(B, H, N, dtype=torch.float16, device=dev)
+        S = qjl_matrix if qjl_matrix.dtype == torch.float32 and qjl_matrix.is_contiguous() else \
+            qjl_matrix.float().contiguous()
+        K.quantize_prod(key_states, _codec_of(rotation, centers, boundaries, bits), S, codes, norms, signs, rnorms)
+        return (PackedTensorMSE(codes, norms, (B, H, N, D), key_states.dtype, int(bits)),
+                PackedQJL(signs, rnorms, D))
+
+    def _decode_keys_qjl_group(self, mse_packed: PackedTensorMSE, qjl: PackedQJL, rotation: torch.Tensor,
+                               centers: torch.Tensor, qjl_matrix: torch.Tensor) -> torch.Tensor:
+        """Q_prod key decoder: MSE reconstruction plus QJL correction (reference :312-330)."""
+        B, H, N, D = mse_packed.original_shape
+        S = qjl_matrix if qjl_matrix.dtype == torch.float32 and qjl_matrix.is_contiguous() else \
+            qjl_matrix.float().contiguous()
+        out = K.dequantize_prod(_packed_rows(mse_packed.packed_indices), _packed_rows(mse_packed.norms),
+                                _packed_rows(qjl.packed_signs), _packed_rows(qjl.residual_norms), N,
+                                _codec_of(rotation, centers, None, mse_packed.bits), S, dim=D)
+        return out.to(mse_packed.original_dtype)
 
     # ------------------------------------------------------------- encoding
     def initialize_from_dense(self, key_states: torch.Tensor, value_states: torch.Tensor, *,
