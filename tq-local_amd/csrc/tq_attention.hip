@@ -57,6 +57,12 @@ constexpr int D = TQ_DIM;
 #ifndef TQ_ATTN_WAVES_G8
 #define TQ_ATTN_WAVES_G8 12
 #endif
+#ifndef TQ_ATTN_NB_G4
+#define TQ_ATTN_NB_G4 1
+#endif
+#ifndef TQ_ATTN_NB_G8
+#define TQ_ATTN_NB_G8 1
+#endif
 #ifndef TQ_ATTN_SETS_G4
 #define TQ_ATTN_SETS_G4 2
 #endif
@@ -69,18 +75,16 @@ struct Cfg {
     static constexpr int NT = NW * 64;
     // per-wave blocks in flight (register sets of packed data)
     static constexpr int NSET = GC == 1 ? TQ_ATTN_SETS_G4 : TQ_ATTN_SETS_G8;
+    // blocks a wave takes through every stage together (NSET is a multiple)
+    static constexpr int NB = GC == 1 ? TQ_ATTN_NB_G4 : TQ_ATTN_NB_G8;
 };
 constexpr int BLK = 16;        // tokens per block (MFMA N)
-// lane-private copies of the key pair table: 32 for the 64-entry (3-bit) table; the 256-entry
-// 4-bit table gets 8 where the value pair table already takes 64 KB of LDS
-template <int KB, bool PV>
-constexpr int KCOPIES = KB <= 3 ? 32 : (PV ? 8 : 32);
-constexpr int WT_STRIDE = 20;  // dwords per row of the weight-transpose buffer (bank spread)
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 constexpr float QJL_SCALE = 1.2533141373155003f / D;  // sqrt(pi/2) / D
 constexpr float LAZY_MAX = 8.0f;                      // log2 headroom before the reference max is raised
+constexpr float WEXP0 = 15.0f;  // f16 exponent bias: a raise puts the largest weight p |v| in [1, 2)
 constexpr int BUF_DW3 = 0x00020000;                   // buffer descriptor word 3 (gfx9: 32-bit untyped)
 #ifndef TQ_KV_NT
 #define TQ_KV_NT 2
@@ -94,10 +98,15 @@ typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f16(const u32x4& a, const u32x4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
 }
 __device__ __forceinline__ i32x4 mfma_i8(const u32x4& a, const u32x4& b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
@@ -156,26 +165,6 @@ __device__ __forceinline__ uint32_t field_x(const uint32_t* w, int pos) {
     return (w[wi] << (S - sh)) & M;
 }
 
-// (byte K of w) & mask in one VALU op (SDWA source byte select); mask lives in a VGPR
-template <int K>
-__device__ __forceinline__ uint32_t and_byte(uint32_t w, uint32_t mask) {
-    if constexpr (K == 0) {
-        return w & mask;
-    } else {
-        uint32_t r;
-        if constexpr (K == 1)
-            asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
-                : "=v"(r) : "v"(mask), "v"(w));
-        else if constexpr (K == 2)
-            asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
-                : "=v"(r) : "v"(mask), "v"(w));
-        else
-            asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
-                : "=v"(r) : "v"(mask), "v"(w));
-        return r;
-    }
-}
-
 // A lane's 24-bit chunk of 3-bit value codes at bit sh of its dword w (sh in {0, 8, 16, 24}),
 // aligned to bit 0: the bits past w come from the next lane of the row of 16 (DPP row_shl:1,
 // lane i reads lane i + 1), whose dword is the following one of the code row wherever the chunk
@@ -226,51 +215,46 @@ struct Rows {
     static constexpr int HPL = GC;  // heads per lane group
     static constexpr int NQJ = GC;  // QJL MFMA sets (four limbs per head in total)
     static constexpr int NH = 4 * GC;
+    // key-score rows: GC = 1 (int8 limbs) 4 h + s, s = limb-product order 0..3; GC = 2 (bf16)
+    // 2 h + x, x = hi | lo part of q_rot.  Lane group g holds rows 4 g .. 4 g + 3.
     __host__ __device__ static constexpr int row(int h, int x) { return GC == 1 ? 4 * h + x : 2 * h + x; }
+    // value rows (head, dim parity p): GC = 1 4 h + 2 p (rows 4 h + 2 p + 1 stay zero), GC = 2
+    // 2 h + p; either way lane group g holds the value rows of the heads whose scores it holds
+    __host__ __device__ static constexpr int vrow(int h, int p) { return GC == 1 ? 4 * h + 2 * p : 2 * h + p; }
 };
 
-// Value MFMA layouts.  Generic: rows (head, w hi|lo), columns = 16 dims, k-slots = 16 tokens
-// x (Cv hi, Cv lo), one 4-byte table lookup per code.  Paired (3- and 4-bit values, at most 4
-// heads): rows (head, dim parity p, w hi|lo) fill all 16 rows, columns = 16 pairs of
-// adjacent dims, k-slots = 8 tokens x parity x (Cv hi, Cv lo); one 8-byte lookup per pair
-// of codes (a code byte at 4 bits, a 6-bit field at 3 bits) returns both dims of a pair,
-// and the A operand is zero where the parities differ.
-template <int VB, int GC>
-constexpr bool PAIRED = GC == 1 && (VB == 4 || VB == 3);
-// Pair-table lookups in the generic layout (5..8 heads, 3- and 4-bit values): lane n's code
-// byte (4-bit) or 6-bit field (3-bit) of dims 8 n + 2 b, 8 n + 2 b + 1 is looked up once, and
-// the two values feed the MFMAs of dims 8 n + 2 b (even) and 8 n + 2 b + 1 (odd), whose
-// column n they both are: half the lookups of one per code, the same MFMAs.
-template <int VB, int GC>
-constexpr bool PAIR_COLS = GC == 2 && (VB == 4 || VB == 3);
-constexpr int VCOPIES = 32;      // lane-private copies of the pair table (bank pair per lane)
-constexpr int WT_STRIDE_P = 36;  // dwords per weight row in the paired layout (32 slots + bank spread)
+// Lookup tables.  Every entry has TCOPIES lane-private copies, copy c in the bank of lane c of a
+// 32-lane LDS pass, so a lookup never conflicts.  Entry e of the pair tables sits at byte 256 e
+// (one v_perm forms a byte code's address): copies 0..31 of the value pair (fp16 Cv[c0],
+// Cv[c1]) at +4 c, and with int8 keys copies 0..31 of the key pair (int8 limbs L0, L1 of
+// Ck[c0], then of Ck[c1]) at +128 + 4 c.  bf16 keys (5..8 heads) keep a table of their own:
+// (Ck hi|lo of c0, Ck hi|lo of c1) per pair, 8 bytes, copy c at +8 c.
+constexpr int TCOPIES = 32;
+constexpr int WROW = 16;  // dwords per row of the weight transpose: 4 lane groups x 4 tokens
+
+template <int KB, int VB>
+constexpr int PAIR_ENTRIES = (1 << (2 * KB)) > (1 << (2 * VB)) ? (1 << (2 * KB)) : (1 << (2 * VB));
 
 // LDS scratch of the image builder
 template <int GC>
 struct PrepLds {
     static constexpr int NH = 4 * GC;
-    float qp[NH][D];  // q S^T of the group's heads
-    float red[16];    // max |q S^T| per matrix-core tile
+    float qp[NH][D];                  // q S^T of the group's heads
+    float qr[GC == 1 ? NH : 1][D];    // q R_k^T times the logit scale (int8 key image)
+    float red[16];                    // max |.| per matrix-core tile: R_k tiles 0..7, S tiles 8..15
 };
 
 template <int KB, int VB, bool QJL, int GC>
 struct Smem {
     static constexpr int NH = 4 * GC;
     static constexpr int NW = Cfg<VB, GC, QJL>::NW;
-    static constexpr bool PV = PAIRED<VB, GC>;
-    static constexpr bool PT = PV || PAIR_COLS<VB, GC>;  // the pair table is built
-    static constexpr int WTS = PV ? WT_STRIDE_P : WT_STRIDE;
-    // both lookup tables sit below 64 KB, so their base folds into the LDS instruction's offset.
-    // (Ck hi|lo of c0, Ck hi|lo of c1) per pair of key codes; KC lane-private copies, entry e of
-    // copy c at byte 8 (KC e + c), so the lanes of a 32-lane LDS pass use distinct bank pairs
-    static constexpr int KC = KCOPIES<KB, PT>;
-    uint2 ktab[1 << (2 * KB)][KC];
-    // paired: (Cv hi|lo of the even dim's code, Cv hi|lo of the odd dim's code) per pair of
-    // codes (2^(2 VB) entries), entry e of copy c at byte 256 e + 8 c from the table base
-    uint2 vtab2[PT ? (1 << (2 * VB)) : 1][PT ? VCOPIES : 1];
-    uint32_t vtab[1 << VB];             // Cv hi|lo per value code (generic layout)
-    uint32_t wt[NW][16][WTS];           // per-wave transpose of the softmax weights
+    static constexpr bool KI8 = GC == 1;
+    static constexpr int PE = KI8 ? PAIR_ENTRIES<KB, VB> : (1 << (2 * VB));
+    static constexpr int KC = KB <= 3 ? 32 : 16;  // copies of the bf16 key pair table
+    // both tables sit below 64 KB, so their bases fold into the LDS instructions' offsets
+    uint2 ktab[KI8 ? 1 : (1 << (2 * KB))][KI8 ? 1 : KC];  // bf16 key pairs
+    uint32_t tab[PE][64];                              // value pairs (and int8 key pairs)
+    uint32_t wt[NW][Cfg<VB, GC, QJL>::NB][16][WROW];   // per-wave transposes of the softmax weights
     union {
         struct {
             uint4 img[IMG_DW / 4];      // this group's q-side image
@@ -428,7 +412,7 @@ __device__ __forceinline__ void split3_bf16(const float4& a, const float4& b, u3
 // operand loads are issued and before they are waited for: global loads complete in issue
 // order, so loads that mid() issues stay in flight through the products (and the barriers,
 // which wait for LDS only).
-template <bool QJL, int GC, int NW, typename Mid>
+template <bool QJL, int GC, int NW, bool KI8, typename Mid>
 __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, int G, int bh0,
                                                const float* __restrict__ Rk, const float* __restrict__ S,
                                                float c_mse, PrepLds<GC>& L, uint32_t* img, uint4* qst,
@@ -495,8 +479,8 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
         }
         // lane (c, kq) holds rows 4 kq + i (query heads) of column j
         const int j = 16 * (t & 7) + c;
-        if (t < 8) {
-            // key-score image: dword (jj, lane (n, gq), r) holds dim j = 32 gq + 4 jj + r of row n
+        if (!KI8 && t < 8) {
+            // bf16 key-score image: dword (jj, lane (n, gq), r) holds dim j = 32 gq + 4 jj + r of row n
             if (4 * kq < NH) {
                 const int gq = j >> 5, jj = (j >> 2) & 7, r = j & 3;
                 uint32_t* base = img + IMG_QA + (jj * 64 + 16 * gq) * 4 + r;
@@ -507,24 +491,30 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
                     const float xh = bf16_val(bf16_bits(x));
                     base[R::row(h, 0) * 4] = dup_bf16(xh);
                     base[R::row(h, 1) * 4] = dup_bf16(x - xh);
-                    if constexpr (GC == 1) {  // rows 4 h + 2, 4 h + 3 are unused
-                        base[R::row(h, 2) * 4] = 0u;
-                        base[R::row(h, 3) * 4] = 0u;
-                    }
                 }
             }
         } else {
+            // q S^T (and with int8 keys q R_k^T times the logit scale) to LDS, with the tile's
+            // max |.| for the fixed-point exponents of phase 2
+            float* dst = &L.qp[0][0];
+            float sc = 1.0f;
+            if constexpr (KI8) {
+                if (t < 8) dst = &L.qr[0][0], sc = c_mse;
+            }
+            float x[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = acc[i] * sc;
             if (4 * kq < NH) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) L.qp[4 * kq + i][j] = acc[i];
+                for (int i = 0; i < 4; ++i) dst[(4 * kq + i) * D + j] = x[i];
             }
-            float mx = fmaxf(fmaxf(fabsf(acc[0]), fabsf(acc[1])), fmaxf(fabsf(acc[2]), fabsf(acc[3])));
+            float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
             mx = row_max16(mx);  // then the four rows of 16 lanes
             mx = fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0)),
                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 16))),
                        fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)),
                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 48))));
-            if (lane == 0) L.red[t - 8] = mx;
+            if (lane == 0) L.red[t] = mx;
         }
     }
 }
@@ -536,7 +526,7 @@ __device__ __forceinline__ int qjl_image(const PrepLds<GC>& L, uint32_t* img, in
     constexpr int NH = 4 * GC;
     float mx = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 8; ++w) mx = fmaxf(mx, L.red[w]);
+    for (int w = 0; w < 8; ++w) mx = fmaxf(mx, L.red[8 + w]);
     int e = 0;
     if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
     int F = 22 - e;
@@ -576,6 +566,45 @@ __device__ __forceinline__ float qjl_combine(const i32x4 (&acc)[GC], int i) {
 }
 
 
+// Phase 2 (after a barrier), int8 key image (at most 4 query heads): x = rint(q_rot 2^F), the
+// q-side score operand (q R_k^T times the logit scale) in fixed point with max |x| < 2^22 (F
+// capped at 60), in three balanced base-256 digits X0..X2.  Key MFMA j, lane (row 4 h + s,
+// group g), byte 4 i + 2 e + m <-> dim d = 32 g + 8 j + 2 i + e and codebook limb m: the A operand
+// is X_{s-m}[h][d] where 0 <= s - m <= 2 and zero otherwise, so row 4 h + s sums the products of
+// digit pairs of weight 2^(8 s).  Returns F in every thread.
+template <int NT>
+__device__ __forceinline__ int key_image_i8(const PrepLds<1>& L, uint32_t* img, int tid) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) mx = fmaxf(mx, L.red[w]);
+    int e = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &e);  // mx < 2^e
+    int F = 22 - e;
+    F = F > 60 ? 60 : F;
+    const float sc = ldexpf(1.0f, F);
+    uint8_t* ib = reinterpret_cast<uint8_t*>(img + IMG_QA);
+    for (int i = tid; i < 4 * D; i += NT) {
+        const int h = i / D, d = i % D;
+        int x = (int)rintf(L.qr[h][d] * sc);
+        int X[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            X[k] = ((x + 128) & 255) - 128;  // balanced base-256 digit k
+            x = (x - X[k]) >> 8;
+        }
+        const int g = d >> 5, j = (d >> 3) & 3, ii = (d >> 1) & 3, par = d & 1;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const int l = s - m;
+                const int v = (l >= 0 && l <= 2) ? X[l] : 0;
+                ib[(j * 64 + 16 * g + 4 * h + s) * 16 + 4 * ii + 2 * par + m] = (uint8_t)(v & 255);
+            }
+    }
+    return F;
+}
+
 template <int KB, int VB, bool QJL, int GC>
 __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
@@ -587,11 +616,13 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
     using Sm = Smem<KB, VB, QJL, GC>;
     using R = Rows<GC>;
+    constexpr bool KI8 = Sm::KI8;
     constexpr int NW = Cfg<VB, GC, QJL>::NW;
     constexpr int NT = Cfg<VB, GC, QJL>::NT;
     constexpr int KROW = D * KB / 8;  // bytes per key row
     constexpr int VROW = D * VB / 8;  // bytes per value row
     constexpr int VCH = 8 * VB;       // bits of one lane's 8-dim value chunk
+    constexpr int NKM = KI8 ? 4 : 8;  // key-score MFMAs per block
     __shared__ Sm sm;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -708,70 +739,100 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // pinned with scheduling barriers here as in the loop: the waits at the loop head hold for
     // both ways in, and first loads issued in another order would force a wait for all of them.
     constexpr int NSET = Cfg<VB, GC, QJL>::NSET;
+    constexpr int NB = Cfg<VB, GC, QJL>::NB;
+    static_assert(NSET % NB == 0, "register sets come in whole steps");
     Kd kset[NSET];
     Vd vset[NSET];
 
     // ------------------------------------------------------------ prologue
-    // phase 1: codebooks (hi|lo) and the group's q-side image (every split workgroup of the
-    // group computes it: the mat-vecs on the matrix cores from L2-resident R_k and S, cheaper
-    // than a separate launch ahead of the split pass)
+    // phase 1: codebooks and the group's q-side products (every split workgroup of the group
+    // computes them: the mat-vecs on the matrix cores from L2-resident R_k and S, cheaper than
+    // a separate launch ahead of the split pass)
     uint32_t* img = reinterpret_cast<uint32_t*>(sm.u.pro.img);
     // every global load of the prologue is issued before any is waited for: the codebook entries
     // (unconditionally, in range), the products' operands, then the first blocks of the token
     // loop, whose HBM latency the rest of the prologue covers
     const float ck_e = Ck[tid & ((1 << KB) - 1)];
     const float cv_e = Cv[tid & ((1 << VB) - 1)];
-    image_products<QJL, GC, NW>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, sm.u.pro.qst[wave], wave, lane, [&] {
+    // int8 keys: the key codebook in fixed point, |Ck| 2^E < 2^15 (wave-uniform scalar loads)
+    int E = 0;
+    if constexpr (KI8) {
+        float cmax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < (1 << KB); ++c) cmax = fmaxf(cmax, fabsf(Ck[c]));
+        int e = 0;
+        if (cmax > 0.0f) (void)frexpf(cmax, &e);  // cmax < 2^e
+        E = 15 - e;
+    }
+    image_products<QJL, GC, NW, KI8>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, sm.u.pro.qst[wave], wave, lane, [&] {
 #pragma unroll
         for (int s = 0; s < NSET; ++s) {
             load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
             __builtin_amdgcn_sched_barrier(0);
         }
     });
-    // lane l holds the hi|lo codebook entries Ck[l mod 2^KB] and Cv[l mod 2^VB]
-    const uint32_t ckp = pack_hilo(ck_e), cvp = pack_hilo(cv_e);
-    if (tid >= 64 && tid < 64 + (1 << VB)) sm.vtab[tid - 64] = cvp;
-    // pair tables from the codebooks in the lanes (ds_bpermute), two neighbouring copies of an
-    // entry per 16-byte write, by the older half of the waves: they finish their products first
-    // and wait at the barrier below for the younger ones anyway.  Every loop runs a multiple of
-    // 64 iterations per stride, so whole waves take part in each permute.
+    // pair tables from the codebook entries in the lanes (lane l holds Ck[l mod 2^KB] and
+    // Cv[l mod 2^VB]; ds_bpermute), four copies of an entry per 16-byte write, by the older half
+    // of the waves: they finish their products first and wait at the barrier below for the
+    // younger ones anyway.  Every loop runs whole waves (strides and bounds are multiples of
+    // 64), so every lane takes part in each permute.
     if (wave < NW / 2) {
         const auto from_lane = [](uint32_t v, int l) {
             return (uint32_t)__builtin_amdgcn_ds_bpermute(l << 2, (int)v);
         };
-        for (int i = tid; i < (1 << (2 * KB)) * Sm::KC / 2; i += NT / 2) {
-            const int e = i / (Sm::KC / 2);
-            const uint32_t lo = from_lane(ckp, e & ((1 << KB) - 1)), hi = from_lane(ckp, e >> KB);
-            reinterpret_cast<uint4*>(&sm.ktab[0][0])[i] = make_uint4(lo, hi, lo, hi);
+        constexpr int QPE = TCOPIES / 4;  // 16-byte writes per entry and table
+        uint4* tab4 = reinterpret_cast<uint4*>(&sm.tab[0][0]);
+        const uint32_t cvh = tq::f32_to_f16(cv_e);
+        constexpr int NV = (1 << (2 * VB)) * QPE;
+        for (int i = tid; i < (NV + 63) / 64 * 64; i += NT / 2) {
+            const int e = i / QPE, qd = i % QPE;
+            const uint32_t v = from_lane(cvh, e & ((1 << VB) - 1)) | (from_lane(cvh, e >> VB) << 16);
+            if (i < NV) tab4[e * 16 + qd] = make_uint4(v, v, v, v);
         }
-        if constexpr (Sm::PT) {
-            for (int i = tid; i < (1 << (2 * VB)) * VCOPIES / 2; i += NT / 2) {
-                const int e = i / (VCOPIES / 2);
-                const uint32_t lo = from_lane(cvp, e & ((1 << VB) - 1)), hi = from_lane(cvp, e >> VB);
-                reinterpret_cast<uint4*>(&sm.vtab2[0][0])[i] = make_uint4(lo, hi, lo, hi);
+        if constexpr (KI8) {
+            // (L0, L1) of Ck in one dword's low half: Ck 2^E = L0 + 256 L1, balanced digits
+            const int ci = (int)rintf(ck_e * ldexpf(1.0f, E));
+            const int l0 = ((ci + 128) & 255) - 128;
+            const uint32_t limbs = (uint32_t)(l0 & 255) | ((uint32_t)(((ci - l0) >> 8) & 255) << 8);
+            constexpr int NK = (1 << (2 * KB)) * QPE;
+            for (int i = tid; i < (NK + 63) / 64 * 64; i += NT / 2) {
+                const int e = i / QPE, qd = i % QPE;
+                const uint32_t v = from_lane(limbs, e & ((1 << KB) - 1)) | (from_lane(limbs, e >> KB) << 16);
+                if (i < NK) tab4[e * 16 + 8 + qd] = make_uint4(v, v, v, v);
+            }
+        } else {
+            const uint32_t ckp = pack_hilo(ck_e);
+            constexpr int NK = (1 << (2 * KB)) * Sm::KC / 2;  // two copies of an entry per write
+            for (int i = tid; i < (NK + 63) / 64 * 64; i += NT / 2) {
+                const int e = i / (Sm::KC / 2);
+                const uint32_t lo = from_lane(ckp, e & ((1 << KB) - 1)), hi = from_lane(ckp, e >> KB);
+                if (i < NK) reinterpret_cast<uint4*>(&sm.ktab[0][0])[i] = make_uint4(lo, hi, lo, hi);
             }
         }
     }
-    // zero slots of the weight transpose (never written by the loop)
-    for (int i = tid; i < NW * 16 * Sm::WTS; i += NT) (&sm.wt[0][0][0])[i] = 0u;
+    // the weight transpose starts zeroed: the loop writes only the halves and rows that hold
+    // weights, the rest of the value MFMAs' A operand stays zero
+    for (int i = tid; i < (int)(sizeof(sm.wt) / 4); i += NT) (&sm.wt[0][0][0][0])[i] = 0u;
     __syncthreads();
-    // phase 2 (LDS only): the QJL limb image
-    int G2 = 0;
-    if constexpr (QJL) {
-        G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid);
-        __syncthreads();
-    }
-    // phase 3: operands into registers.  A operands of the key-score MFMAs (32 VGPRs): lane
-    // (n, g), MFMA j, VGPR r holds q_x[h][32 g + 4 j + r] twice (k-slots for the hi and lo
-    // codebook parts).
-    u32x4 qa[8];
+    // phase 2 (LDS only): the QJL limb image and the int8 key image
+    int G2 = 0, F = 0;
+    if constexpr (QJL) G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid);
+    if constexpr (KI8) F = key_image_i8<NT>(sm.u.pro.ps, img, tid);
+    if constexpr (QJL || KI8) __syncthreads();
+    // phase 3: operands into registers.  A operands of the key-score MFMAs: int8 keys, lane
+    // (row 4 h + s, g), MFMA j: digits of dims 32 g + 8 j .. + 7 (16 VGPRs); bf16 keys, lane
+    // (n, g), MFMA j, VGPR r holds q_x[h][32 g + 4 j + r] twice (32 VGPRs).
+    u32x4 qa[NKM];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qa[j] = *reinterpret_cast<const u32x4*>(img + IMG_QA + (j * 64 + lane) * 4);
+    for (int j = 0; j < NKM; ++j) qa[j] = *reinterpret_cast<const u32x4*>(img + IMG_QA + (j * 64 + lane) * 4);
+    // scores come out of the key MFMAs in units of kscale (int8: 2^-(F + E)) and are taken to
+    // log2 units by an fma that is already there; the QJL term is scaled to the same units
+    const float kscale = KI8 ? ldexpf(1.0f, -(F + E)) : 1.0f;
     // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
     // 32 g + 4 jj + v + 8 e.
     u32x4 qj[R::NQJ][2];
     float sq[R::HPL];
-    float qfix = 0.0f;  // QJL logit per unit of sum_{s_d = 1} y_d (y_d = q_proj_d 2^G2 to rounding)
+    float qfix = 0.0f;  // QJL logit (in score units) per unit of sum_{s_d = 1} y_d
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) sq[i] = 0.0f;
     if constexpr (QJL) {
@@ -782,7 +843,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                 qj[set][jj] = *reinterpret_cast<const u32x4*>(img + IMG_QJ + ((set * 2 + jj) * 64 + lane) * 4);
         // sum_d q_proj s_d = 2 sum_{s_d = 1} q_proj - sum_d q_proj; sum_d y_d is the QJL MFMA
         // against a token whose sign bits are all set (the same arithmetic as every token's sum)
-        qfix = ldexpf(1.0f, 1 - G2) * c_qjl;
+        qfix = ldexpf(c_qjl, 1 - G2 + (KI8 ? F + E : 0));
         u32x4 ones[2];
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
@@ -798,313 +859,249 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         for (int i = 0; i < R::HPL; ++i) sq[i] = qjl_combine<GC>(acc_all, i) * (0.5f * qfix);
     }
 
-    // per-lane softmax state (heads of this lane group) and value accumulators
-    float m_ref[R::HPL], s_lane[R::HPL];
+    // per-lane softmax state (heads of this lane group) and value accumulators.  The reference
+    // maximum m_ref tracks max(score + e_v) - WEXP0, e_v = the biased f16 exponent of the value
+    // norm, so that the largest weight p |v| entering the fp16 value MFMAs is ~1 after a raise and
+    // at most 2^(LAZY_MAX + 1) before the next: the fp16 weights neither overflow nor lose their
+    // leading bits, whatever the value norms.
+    float m_ref[R::HPL], s_lane[R::HPL], m_thr[R::HPL];
 #pragma unroll
-    for (int i = 0; i < R::HPL; ++i) m_ref[i] = NEG_INF, s_lane[i] = 0.0f;
-    float m_thr[R::HPL];  // m_ref + LAZY_MAX
+    for (int i = 0; i < R::HPL; ++i) m_ref[i] = NEG_INF, s_lane[i] = 0.0f, m_thr[i] = NEG_INF;
+    // one set of value accumulators per block of a step (independent MFMA chains)
+    f32x4 acc_v[NB][4];
 #pragma unroll
-    for (int i = 0; i < R::HPL; ++i) m_thr[i] = NEG_INF;
-    constexpr bool PV = Sm::PV;
-    constexpr int NACC = PV ? 4 : 8;  // value accumulators: column groups of 16 pairs / 16 dims
-    f32x4 acc_v[NACC];
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int m = 0; m < NACC; ++m) acc_v[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < 4; ++m) acc_v[b][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    uint32_t(*wt)[Sm::WTS] = sm.wt[wave];
-    // generic layout: token 4 r + g sits at k-slot pair 4 g + r
+    const uint32_t plane = 4u * (uint32_t)(lane & (TCOPIES - 1));        // value copy: +4 c
+    const uint32_t kplane = KI8 ? 128u + plane : 8u * (uint32_t)(lane & (Sm::KC - 1));  // key copy
+    constexpr int KSHIFT = KI8 ? 8 : (Sm::KC == 32 ? 8 : 7);  // log2 bytes per key-table entry row
+    // the weight of token n = 4 i + k lands in dword i of lane group k's slots
     const int wslot = 4 * (n & 3) + (n >> 2);
-    // paired layout: token n = 8 u + 4 s + k (u: MFMA half, k: lane group, s: which of its
-    // two tokens) -> dwords 4 (4 u + k) + 2 s + p of rows (head, p, x)
-    const int pslot = 4 * (4 * (n >> 3) + (n & 3)) + 2 * ((n >> 2) & 1);
-    const uint32_t plane = 8u * (uint32_t)(lane & (VCOPIES - 1));  // copy of the pair table
-    constexpr int KSHIFT = Sm::KC == 32 ? 8 : (Sm::KC == 8 ? 6 : 3);  // log2 bytes per key-table entry row
-    const uint32_t klane = 8u * (uint32_t)(lane & (Sm::KC - 1));
 
-    // The value MFMAs' A operand for one block: the softmax weights, transposed through LDS
-    // (paired layout: one u32x4 per MFMA half)
-    constexpr int NAV = PV ? 2 : 1;
-    struct Av {
-        u32x4 a[NAV];
-    };
-
-    // ---- score stage, part 1: key-score and QJL MFMAs, then the scores (log2 domain) of
-    // token n for this lane's heads, -inf for tokens past the range.  Returns whether any
-    // score exceeds its head's lazy threshold (wave-uniform).
-    auto scores = [&](const Kd& B, int rel, float (&lg)[R::HPL]) -> bool {
-        // ---- key scores: 8 MFMAs over dims 32 g + 4 j + r
-        // two independent accumulation chains (even / odd j) halve the dependent MFMA latency
-        f32x4 acc_k = f32x4{0.f, 0.f, 0.f, 0.f}, acc_k1 = f32x4{0.f, 0.f, 0.f, 0.f};
-        // the MFMA stages (keys + QJL, values) run at raised wave priority: a wave that reaches
-        // its matrix work issues ahead of waves in their VALU/LDS phases, so the SIMD's MFMA
-        // and VALU work of different waves overlap more (-2.4% per call at C2, -2.5 to -3% at
-        // the other shapes)
+    // One step: NB blocks of this wave (register sets s0 .. s0 + NB - 1, blocks rel0, rel0 + STEP,
+    // ...) through every stage together, so each stage has NB independent chains of lookups and
+    // MFMAs to interleave.  Blocks past the range have all their tokens masked.
+    //   scores   key-score and QJL MFMAs, then the scores (in units of kscale) of token n for this
+    //            lane's heads, -inf past the range;
+    //   raise    (rare, wave-uniform) the lazy reference maximum raised, partial sums and value
+    //            accumulators rescaled;
+    //   weights  p |v| of token n in fp16 into the value MFMAs' A operand, transposed through
+    //            this wave's LDS rows (one wave's LDS accesses execute in order and the compiler
+    //            keeps the may-alias writes and reads of wt in program order, so no fence is
+    //            needed): row vrow(h, p), dword i of lane group k holds token 4 i + k's weight in
+    //            half p;
+    //   values   4 fp16 MFMAs per block, MFMA u over the dim pairs (8 c + 2 u, 8 c + 2 u + 1) of
+    //            column c; lane (c, k) supplies tokens 4 i + k, each one pair-table lookup
+    //            returning the (even, odd) values in k-slot order.
+    // The MFMA stages run at raised wave priority: a wave that reaches its matrix work issues
+    // ahead of waves in their VALU/LDS phases, so the SIMD's MFMA and VALU work of different
+    // waves overlap more.
+    auto process = [&](int s0, int rel0) {
+        float lg[NB][R::HPL];
+        float ev[NB];
+        i32x4 acc_i[NB];
+        f32x4 acc_k[NB], acc_k1[NB];
+        i32x4 acc_q[NB][R::NQJ];
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            u32x4 bk;
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                const uint32_t off = field_x<2 * KB, KSHIFT>(B.kw, (4 * j + 2 * p) * KB) | klane;
-                const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.ktab) + off);
-                bk[2 * p] = e.x;
-                bk[2 * p + 1] = e.y;
-            }
-            if (j & 1)
-                acc_k1 = mfma_bf16(qa[j], bk, acc_k1);
-            else
-                acc_k = mfma_bf16(qa[j], bk, acc_k);
+        for (int b = 0; b < NB; ++b) {
+            acc_i[b] = i32x4{0, 0, 0, 0};
+            acc_k[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            acc_k1[b] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        // ---- QJL sums
-        i32x4 acc_q[R::NQJ];
+        if constexpr (KI8) {
+            // 4 int8 MFMAs per block, dims 32 g + 8 j + 2 i + e: one 4-byte lookup per pair of codes
+            // returns both codes' limbs in k-slot order
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const Kd& B = kset[s0 + b];
+                    u32x4 bk;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        uint32_t off;
+                        if constexpr (KB == 4) {
+                            // code byte i of dword j: LDS byte offset 256 * byte + kplane in one v_perm
+                            off = __builtin_amdgcn_perm(B.kw[j], kplane, 0x0C0C0000u | ((4u + (uint32_t)i) << 8));
+                        } else {
+                            off = field_x<2 * KB, 8>(B.kw, KB * (8 * j + 2 * i)) | kplane;
+                        }
+                        bk[i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.tab) + off);
+                    }
+                    acc_i[b] = mfma_i8(qa[j], bk, acc_i[b]);
+                }
+            }
+        } else {
+            // 8 bf16 MFMAs per block over dims 32 g + 4 j + r; two chains per block
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const Kd& B = kset[s0 + b];
+                    u32x4 bk;
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        const uint32_t off = field_x<2 * KB, KSHIFT>(B.kw, (4 * j + 2 * p) * KB) | kplane;
+                        const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.ktab) + off);
+                        bk[2 * p] = e.x;
+                        bk[2 * p + 1] = e.y;
+                    }
+                    if (j & 1)
+                        acc_k1[b] = mfma_bf16(qa[j], bk, acc_k1[b]);
+                    else
+                        acc_k[b] = mfma_bf16(qa[j], bk, acc_k[b]);
+                }
+            }
+        }
         if constexpr (QJL) {
-            u32x4 bq[2];
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
+            for (int b = 0; b < NB; ++b) {
+                u32x4 bq[2];
 #pragma unroll
-                for (int v = 0; v < 4; ++v) bq[jj][v] = B.sw & (0x01010101u << (4 * jj + v));
+                for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-            for (int set = 0; set < R::NQJ; ++set) {
-                acc_q[set] = mfma_i8(qj[set][0], bq[0], i32x4{0, 0, 0, 0});
-                acc_q[set] = mfma_i8(qj[set][1], bq[1], acc_q[set]);
+                    for (int v = 0; v < 4; ++v) bq[jj][v] = kset[s0 + b].sw & (0x01010101u << (4 * jj + v));
+#pragma unroll
+                for (int set = 0; set < R::NQJ; ++set) {
+                    acc_q[b][set] = mfma_i8(qj[set][0], bq[0], i32x4{0, 0, 0, 0});
+                    acc_q[b][set] = mfma_i8(qj[set][1], bq[1], acc_q[b][set]);
+                }
             }
         }
         __builtin_amdgcn_s_setprio(0);
-        // valid tokens of the block: a scalar count, one compare per lane
-        const int nvalid = __builtin_amdgcn_readfirstlane(nt - rel < BLK ? nt - rel : BLK);
-        const bool valid = n < nvalid;
-        // the f16 norms enter v_fma_mix_f32 as they are (no separate conversions)
-        const float knf = tq::f16_to_f32(B.kn);
-        const float krf = QJL ? tq::f16_to_f32(B.kr) : 0.0f;
+        // ---- scores
         bool over = false;
 #pragma unroll
-        for (int i = 0; i < R::HPL; ++i) {
-            const float ksum = (acc_k[2 * i] + acc_k1[2 * i]) + (acc_k[2 * i + 1] + acc_k1[2 * i + 1]);
-            float v;
-            if constexpr (QJL) {
-                const float qi = qjl_combine<GC>(acc_q, i);  // sum_d y_d s_d
-                v = __builtin_fmaf(knf, ksum, __builtin_fmaf(krf, __builtin_fmaf(qi, qfix, -sq[i]), 0.0f));
-            } else {
-                v = knf * ksum;
-            }
-            lg[i] = valid ? v : NEG_INF;
-            over |= lg[i] > m_thr[i];
-        }
-        return __builtin_amdgcn_ballot_w64(over) != 0;
-    };
-
-    // ---- the lazy reference maximum raised (rare): partial sums and value accumulators
-    // rescaled to the new maximum
-    auto raise_max = [&](const float (&lg)[R::HPL]) {
-#pragma unroll
-        for (int i = 0; i < R::HPL; ++i) {
-            const float mn = fmaxf(m_ref[i], row_max16(lg[i]));
-            const float a = m_ref[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_ref[i] - mn);  // 1 if unchanged
-            s_lane[i] *= a;
-            if constexpr (PV) {
-#pragma unroll
-                for (int m = 0; m < NACC; ++m) acc_v[m] *= a;  // all four rows are this lane's head
-            } else {
-#pragma unroll
-                for (int m = 0; m < NACC; ++m) {
-                    acc_v[m][2 * i] *= a;
-                    acc_v[m][2 * i + 1] *= a;
-                }
-            }
-            m_ref[i] = mn;
-            m_thr[i] = mn + LAZY_MAX;
-        }
-    };
-
-    // ---- score stage, part 2: the softmax weights p |v| of token n (hi and lo bf16 parts)
-    // into the value MFMAs' A operand, transposed through this wave's LDS rows (one wave's
-    // LDS accesses execute in order and the compiler keeps the may-alias writes and reads of
-    // wt in program order, so no fence is needed)
-    auto weights = [&](const float (&lg)[R::HPL], uint32_t vn_bits, Av& av) {
-        const float vnf = tq::f16_to_f32(vn_bits);  // invalid tokens have p = 0
-        uint32_t wq[R::HPL][2];
-#pragma unroll
-        for (int i = 0; i < R::HPL; ++i) {
-            const float p = __builtin_amdgcn_exp2f(lg[i] - m_ref[i]);  // m_ref finite once a block is seen
-            s_lane[i] += p;
-            const float w = __builtin_fmaf(vnf, p, 0.0f);  // p, vnf >= 0
-            // (hi, hi) by one conversion; hi as fp32 is its high half
-            const uint32_t hh = __builtin_bit_cast(uint32_t, bf16x2{(__bf16)w, (__bf16)w});
-            wq[i][0] = hh;
-            wq[i][1] = dup_bf16(w - __uint_as_float(hh & 0xFFFF0000u));
-        }
-        if constexpr (PV) {
-            // rows 4 h + 2 p + x: this lane's head is g; the zero slots are never written
-            wt[4 * g + 0][pslot] = wq[0][0];
-            wt[4 * g + 1][pslot] = wq[0][1];
-            wt[4 * g + 2][pslot + 1] = wq[0][0];
-            wt[4 * g + 3][pslot + 1] = wq[0][1];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) av.a[u] = *reinterpret_cast<const u32x4*>(&wt[n][4 * (4 * u + g)]);
-        } else {
+        for (int b = 0; b < NB; ++b) {
+            const Kd& B = kset[s0 + b];
+            const int rel = rel0 + b * STEP;
+            // valid tokens of the block: a scalar count, one compare per lane
+            const int nvalid = __builtin_amdgcn_readfirstlane(nt - rel < BLK ? nt - rel : BLK);
+            const bool valid = n < nvalid;
+            // the f16 norms enter v_fma_mix_f32 as they are (no separate conversions)
+            const float knf = tq::f16_to_f32(B.kn);
+            const float krf = QJL ? tq::f16_to_f32(B.kr) : 0.0f;
+            ev[b] = (float)__builtin_amdgcn_ubfe(B.vn, 10, 5);  // biased exponent of the value norm
 #pragma unroll
             for (int i = 0; i < R::HPL; ++i) {
-                const int h = R::HPL * g + i;
-                wt[R::row(h, 0)][wslot] = wq[i][0];
-                wt[R::row(h, 1)][wslot] = wq[i][1];
+                float ksum;
+                if constexpr (KI8) {
+                    // sum_s 2^(8 s) row_s: pairs exact in int32 (|row_s| <= 2^22), then one fp32 rounding
+                    const int lo = acc_i[b][0] + (acc_i[b][1] << 8), hi = acc_i[b][2] + (acc_i[b][3] << 8);
+                    ksum = __builtin_fmaf((float)hi, 65536.0f, (float)lo);
+                } else {
+                    ksum = (acc_k[b][2 * i] + acc_k1[b][2 * i]) + (acc_k[b][2 * i + 1] + acc_k1[b][2 * i + 1]);
+                }
+                float v;
+                if constexpr (QJL) {
+                    const float qi = qjl_combine<GC>(acc_q[b], i);  // sum_d y_d s_d
+                    v = __builtin_fmaf(knf, ksum, __builtin_fmaf(krf, __builtin_fmaf(qi, qfix, -sq[i]), 0.0f));
+                } else {
+                    v = knf * ksum;
+                }
+                lg[b][i] = valid ? v : NEG_INF;
+                over |= __builtin_fmaf(lg[b][i], kscale, ev[b]) > m_thr[i];
             }
-            av.a[0] = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
         }
-    };
-
-    // ---- value stage: the value MFMAs of one block
-    auto values = [&](const Vd& B, const Av& av) {
-        __builtin_amdgcn_s_setprio(1);
-        if constexpr (PV && VB == 3) {
-            // paired, 3-bit: lane (c = n, k = g) supplies tokens 8 u + 4 s + g; the 24-bit chunk of
-            // dims 8 c .. 8 c + 7 is aligned to bit 0, and pair m (dims 8 c + 2 m, 8 c + 2 m + 1)
-            // is its 6-bit field m: LDS byte offset 256 * field + plane in two VALU ops
-            uint32_t ch[4];
+        // ---- the lazy reference maximum raised (rare)
+        if (__builtin_amdgcn_ballot_w64(over) != 0) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                ch[r] = chunk3(B.vw[r], vsh);
+            for (int i = 0; i < R::HPL; ++i) {
+                float t = __builtin_fmaf(lg[0][i], kscale, ev[0]);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+                for (int b = 1; b < NB; ++b) t = fmaxf(t, __builtin_fmaf(lg[b][i], kscale, ev[b]));
+                const float mn = fmaxf(m_ref[i], row_max16(t) - WEXP0);
+                const float a = m_ref[i] == NEG_INF ? 0.0f : __builtin_amdgcn_exp2f(m_ref[i] - mn);  // 1 if unchanged
+                s_lane[i] *= a;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const uint32_t o0 = field_x<6, 8>(&ch[2 * u], 6 * m) | plane;
-                    const uint32_t o1 = field_x<6, 8>(&ch[2 * u + 1], 6 * m) | plane;
-                    const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
-                    const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
-                    acc_v[m] = mfma_bf16(av.a[u], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
-                }
-            }
-        } else if constexpr (PV) {
-            // paired, 4-bit: lane (c = n, k = g) supplies tokens 8 u + 4 s + g, pair column c of
-            // group m = code byte m of dword c (dims 8 c + 2 m, 8 c + 2 m + 1)
+                for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    // LDS byte offset 256 * byte m + plane in one v_perm: [plane, byte m, 0, 0]
-                    constexpr uint32_t SEL_LO = 0x0C0C0000u;
-                    const uint32_t sel = SEL_LO | ((4u + (uint32_t)m) << 8);
-                    const uint32_t o0 = __builtin_amdgcn_perm(B.vw[2 * u], plane, sel);
-                    const uint32_t o1 = __builtin_amdgcn_perm(B.vw[2 * u + 1], plane, sel);
-                    const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
-                    const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
-                    acc_v[m] = mfma_bf16(av.a[u], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
-                }
-            }
-        } else if constexpr (PAIR_COLS<VB, GC> && VB == 4) {
-            // generic layout, 4-bit: one pair-table lookup per two tokens of one dim.  Lane (n, g)
-            // supplies tokens 4 r + g (k-slots 8 g + 2 r + y); byte b of tp[k][par] holds the codes
-            // of dim 8 n + 2 b + par of tokens 4 (2 k) + g (low nibble) and 4 (2 k + 1) + g (high
-            // nibble), so a lookup returns the (Cv hi|lo) dwords of two consecutive k-slot pairs of
-            // one MFMA operand, in register order
-            uint32_t tp[2][2];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const uint32_t a = B.vw[2 * k], b = B.vw[2 * k + 1];
-                tp[k][0] = (a & 0x0F0F0F0Fu) | ((b << 4) & 0xF0F0F0F0u);
-                tp[k][1] = ((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u);
-            }
-#pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                // LDS byte offset 256 * byte (m / 2) + plane in one v_perm: [plane, byte, 0, 0]
-                const uint32_t sel = 0x0C0C0000u | ((4u + (uint32_t)(m >> 1)) << 8);
-                const uint32_t o0 = __builtin_amdgcn_perm(tp[0][m & 1], plane, sel);
-                const uint32_t o1 = __builtin_amdgcn_perm(tp[1][m & 1], plane, sel);
-                const uint2 e0 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o0);
-                const uint2 e1 = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o1);
-                acc_v[m] = mfma_bf16(av.a[0], u32x4{e0.x, e0.y, e1.x, e1.y}, acc_v[m]);
-            }
-        } else if constexpr (PAIR_COLS<VB, GC>) {
-            // generic layout, one pair-table lookup per two codes: lane (n, g) supplies tokens
-            // 4 r + g (k-slots 8 g + 2 r + y); pair b of its 8-dim chunk feeds MFMAs 2 b and 2 b + 1
-            uint32_t ch[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if constexpr (VB == 3)
-                    ch[r] = chunk3(B.vw[r], vsh);
-                else
-                    ch[r] = B.vw[r];
-            }
-#pragma unroll
-            for (int pb = 0; pb < 4; ++pb) {
-                uint2 e[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    uint32_t o;
-                    if constexpr (VB == 4) {
-                        // LDS byte offset 256 * byte pb + plane in one v_perm: [plane, byte pb, 0, 0]
-                        o = __builtin_amdgcn_perm(ch[r], plane, 0x0C0C0000u | ((4u + (uint32_t)pb) << 8));
-                    } else {
-                        o = field_x<6, 8>(&ch[r], 6 * pb) | plane;
+                    for (int m = 0; m < 4; ++m) {
+                        if constexpr (GC == 1) {
+                            acc_v[b][m] *= a;  // the lane's four rows are its head's (two of them zero)
+                        } else {
+                            acc_v[b][m][2 * i] *= a;
+                            acc_v[b][m][2 * i + 1] *= a;
+                        }
                     }
-                    e[r] = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.vtab2) + o);
                 }
-                acc_v[2 * pb] = mfma_bf16(av.a[0], u32x4{e[0].x, e[1].x, e[2].x, e[3].x}, acc_v[2 * pb]);
-                acc_v[2 * pb + 1] = mfma_bf16(av.a[0], u32x4{e[0].y, e[1].y, e[2].y, e[3].y}, acc_v[2 * pb + 1]);
+                m_ref[i] = mn;
+                m_thr[i] = mn + (WEXP0 + LAZY_MAX);
             }
-        } else {
-            // lane (n, g) supplies tokens 4 r + g (k-slots 8 g + 2 r + y), dim 8 n + m
-            uint32_t vch[4][2];  // VB = 4: [r][0] = chunk << 2 (even codes), [r][1] = chunk >> 2 (odd codes)
+        }
+        // ---- weights
+        u32x4 av[NB];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if constexpr (VB == 3)
-                    vch[r][0] = chunk3(B.vw[r], vsh);
-                else
-                    vch[r][0] = B.vw[r] >> vsh;
-                if constexpr (VB == 4) {
-                    vch[r][1] = vch[r][0] >> 2;
-                    vch[r][0] = vch[r][0] << 2;
-                }
+        for (int b = 0; b < NB; ++b) {
+            uint32_t(*wt)[WROW] = sm.wt[wave][b];
+            const float vnf = tq::f16_to_f32(kset[s0 + b].vn);  // invalid tokens have p = 0
+#pragma unroll
+            for (int i = 0; i < R::HPL; ++i) {
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[b][i], kscale, -m_ref[i]));
+                s_lane[i] += p;
+                const uint16_t w = (uint16_t)tq::f32_to_f16(__builtin_fmaf(vnf, p, 0.0f));
+                const int h = R::HPL * g + i;
+                reinterpret_cast<uint16_t*>(&wt[R::vrow(h, 0)][wslot])[0] = w;
+                reinterpret_cast<uint16_t*>(&wt[R::vrow(h, 1)][wslot])[1] = w;
             }
-            const uint32_t m3c = __builtin_amdgcn_readfirstlane(0x3Cu);
-            auto vmfma = [&](auto mc) {
-                constexpr int m = decltype(mc)::value;
+            av[b] = *reinterpret_cast<const u32x4*>(&wt[n][4 * g]);
+        }
+        // ---- values
+        __builtin_amdgcn_s_setprio(1);
+        uint32_t ch[NB][4];  // the lane's chunk of each token, aligned to bit 0 (VB < 4)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w = vset[s0 + b].vw[i];
+                if constexpr (VB == 3)
+                    ch[b][i] = chunk3(w, vsh);
+                else if constexpr (VB < 3)
+                    ch[b][i] = w >> vsh;
+                else
+                    ch[b][i] = w;
+            }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
                 u32x4 bv;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
+                for (int i = 0; i < 4; ++i) {
                     uint32_t off;
                     if constexpr (VB == 4) {
-                        // 4 * code m = byte m/2 of (chunk << 2 if m even, chunk >> 2 if odd) & 0x3C
-                        off = and_byte<(m >> 1)>(vch[r][m & 1], m3c);
+                        // code byte u: LDS byte offset 256 * byte + plane in one v_perm
+                        off = __builtin_amdgcn_perm(ch[b][i], plane, 0x0C0C0000u | ((4u + (uint32_t)u) << 8));
                     } else {
-                        off = field_x<VB, 2>(&vch[r][0], VB * m);
+                        off = field_x<2 * VB, 8>(&ch[b][i], 2 * VB * u) | plane;
                     }
-                    bv[r] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.vtab) + off);
+                    bv[i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.tab) + off);
                 }
-                acc_v[m] = mfma_bf16(av.a[0], bv, acc_v[m]);
-            };
-            vmfma(std::integral_constant<int, 0>{});
-            vmfma(std::integral_constant<int, 1>{});
-            vmfma(std::integral_constant<int, 2>{});
-            vmfma(std::integral_constant<int, 3>{});
-            vmfma(std::integral_constant<int, 4>{});
-            vmfma(std::integral_constant<int, 5>{});
-            vmfma(std::integral_constant<int, 6>{});
-            vmfma(std::integral_constant<int, 7>{});
+                acc_v[b][u] = mfma_f16(av[b], bv, acc_v[b][u]);
+            }
         }
         __builtin_amdgcn_s_setprio(0);
     };
 
     // (the first NSET blocks were issued in the prologue)
     if (nb > 0) {
-        auto process = [&](const Kd& K_, const Vd& V_, int rel) {
-            float lg[R::HPL];
-            if (scores(K_, rel, lg)) raise_max(lg);
-            Av av;
-            weights(lg, K_.vn, av);
-            values(V_, av);
-        };
-        // whole rounds of NSET blocks: up to NSET - 1 blocks past the range end the wave's last
-        // round, and a wave-uniform branch skips their processing (not their refill loads, which
-        // stay unconditional).  Skipping matters where a workgroup's blocks do not divide
-        // evenly among its waves (C4: 128 blocks over 12 waves, -0.8 us per call; C5 shape -1.4)
+        // whole rounds of NSET blocks, NB per step: up to NSET - 1 blocks past the range end the
+        // wave's last round, and a wave-uniform branch skips a step whose first block is past it
+        // (not the refill loads, which stay unconditional).  Skipping matters where a workgroup's
+        // blocks do not divide evenly among its waves (C4: 128 blocks over 12 waves, -0.8 us per
+        // call; C5 shape -1.4)
         for (int i = 0; i < nb; i += NSET) {
 #pragma unroll
-            for (int s = 0; s < NSET; ++s) {
+            for (int s = 0; s < NSET; s += NB) {
                 const int rel = first + (i + s) * STEP;
-                if (rel < nt) process(kset[s], vset[s], rel);
+                if (rel < nt) process(s, rel);
                 __builtin_amdgcn_sched_barrier(0);
-                load_k(kset[s], rel + NSET * STEP), load_v(vset[s], rel + NSET * STEP);
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    load_k(kset[s + b], rel + (NSET + b) * STEP), load_v(vset[s + b], rel + (NSET + b) * STEP);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -1115,20 +1112,21 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     float s_row[R::HPL];
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) s_row[i] = row_sum16(s_lane[i]);
-    // generic: lane (n, g) holds dims 8 n + m of heads R::HPL g + i; paired: lane (n, g) holds
-    // head g, dims 8 n + 2 m + p in rows (p, x) = (r >> 1, r & 1)
+    // lane (n, g) holds dims 8 n + 2 u + p of heads R::HPL g + i: accumulator u, register 2 p
+    // (GC = 1; registers 1 and 3 are the zero rows) or 2 i + p (GC = 2)
 #pragma unroll
     for (int i = 0; i < R::HPL; ++i) {
         const int h = R::HPL * g + i;
-        if constexpr (PV) {
 #pragma unroll
-            for (int m = 0; m < NACC; ++m) {
-                sm.u.epi.o[wave][h][8 * n + 2 * m] = acc_v[m][0] + acc_v[m][1];
-                sm.u.epi.o[wave][h][8 * n + 2 * m + 1] = acc_v[m][2] + acc_v[m][3];
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int r = GC == 1 ? 2 * p : 2 * i + p;
+                float o = acc_v[0][u][r];
+#pragma unroll
+                for (int b = 1; b < NB; ++b) o += acc_v[b][u][r];
+                sm.u.epi.o[wave][h][8 * n + 2 * u + p] = o;
             }
-        } else {
-#pragma unroll
-            for (int m = 0; m < NACC; ++m) sm.u.epi.o[wave][h][8 * n + m] = acc_v[m][2 * i] + acc_v[m][2 * i + 1];
         }
         if (n == 0) {
             sm.u.epi.m[wave][h] = m_ref[i];
