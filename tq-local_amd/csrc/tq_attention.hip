@@ -170,7 +170,7 @@ __device__ __forceinline__ uint32_t field_x(const uint32_t* w, int pos) {
 // lane i reads lane i + 1), whose dword is the following one of the code row wherever the chunk
 // straddles.  Bits 24..31 of the result are not part of the chunk.
 __device__ __forceinline__ uint32_t chunk3(uint32_t w, int sh) {
-    const uint32_t next = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w, 0x101, 0xF, 0xF, false);
+    const uint32_t next = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x101, 0xF, 0xF, true);
     return __builtin_amdgcn_alignbit(next, w, sh);
 }
 
@@ -249,13 +249,21 @@ struct Smem {
     static constexpr int NH = 4 * GC;
     static constexpr int NW = Cfg<VB, GC, QJL>::NW;
     static constexpr bool KI8 = GC == 1;
-    static constexpr int PE = KI8 ? PAIR_ENTRIES<KB, VB> : (1 << (2 * VB));
+    // Byte windows (3-bit codes): the 6-bit field of a code pair is looked up by a byte of the
+    // packed words that holds it, one v_perm per lookup.  T0 (the pair tables) is indexed by a
+    // byte whose bits 0..5 hold the pair, T2 by a byte whose bits 2..7 hold it; the two spare
+    // bits belong to neighbouring codes, so each pair has 4 entries in either table.
+    static constexpr bool KWIN = KI8 && KB == 3;
+    static constexpr bool VWIN = VB == 3;
+    static constexpr bool WIN = KWIN || VWIN;
+    static constexpr int PE = WIN ? 256 : (KI8 ? PAIR_ENTRIES<KB, VB> : (1 << (2 * VB)));
     static constexpr int KC = KB <= 3 ? 32 : 16;  // copies of the bf16 key pair table
-    // both tables sit below 64 KB, so their bases fold into the LDS instructions' offsets
-    uint2 ktab[KI8 ? 1 : (1 << (2 * KB))][KI8 ? 1 : KC];  // bf16 key pairs
-    uint32_t tab[PE][64];                              // value pairs (and int8 key pairs)
-    uint32_t wt[NW][Cfg<VB, GC, QJL>::NB][16][WROW];   // per-wave transposes of the softmax weights
+    // ktab and tab sit below 64 KB, so their bases fold into the LDS instructions' offsets; T2
+    // starts exactly 64 KB above T0 (a lookup adds the 64 KB through byte 2 of its address)
+    uint2 ktab[KI8 ? 2 : (1 << (2 * KB))][KI8 ? 1 : KC];  // bf16 key pairs (int8 keys: padding)
+    uint32_t tab[PE][64];                              // value pairs (and int8 key pairs): T0
     union {
+        uint32_t t2[WIN ? 256 : 1][64];                // T2, built over the prologue's area
         struct {
             uint4 img[IMG_DW / 4];      // this group's q-side image
             uint4 qst[NW][NH * 16];     // per-wave copy of the group's query rows
@@ -266,9 +274,22 @@ struct Smem {
             float m[NW][NH];
             float s[NW][NH];
         } epi;
-
     } u;
+    uint32_t wt[NW][Cfg<VB, GC, QJL>::NB][16][WROW];   // per-wave transposes of the softmax weights
 };
+
+// LDS byte offset (from T0's base) of the table entry of the 6-bit field at bit p of the word
+// array w, p a compile-time constant after unrolling.  s is the stream w >> 4 (s[i] = bits
+// 32 i + 4 .. 32 i + 35 of w), needed for fields at p = 4, 6 mod 8 only.  pl is the lane's copy
+// offset (byte 0) with byte 2 = 1: the selector copies byte 0 and, for T2, byte 2 (+64 KB).
+__device__ __forceinline__ uint32_t win_off(const uint32_t* w, const uint32_t* s, int p, uint32_t pl) {
+    const bool sh = (p & 7) >= 4;
+    const int q = sh ? p - 4 : p;             // 0 or 2 mod 8 in w or s
+    const bool t2 = (q & 7) == 2;
+    const int wb = t2 ? q - 2 : q;            // first bit of the byte window
+    const uint32_t sel = (t2 ? 0x0C020000u : 0x0C0C0000u) | ((4u + (uint32_t)((wb & 31) >> 3)) << 8);
+    return __builtin_amdgcn_perm(sh ? s[wb >> 5] : w[wb >> 5], pl, sel);
+}
 
 // ----------------------------------------------------------------- merge
 // One query head bh, MT threads (t = 0..MT-1): merge the split partials (maxima in the log2
@@ -783,10 +804,12 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         constexpr int QPE = TCOPIES / 4;  // 16-byte writes per entry and table
         uint4* tab4 = reinterpret_cast<uint4*>(&sm.tab[0][0]);
         const uint32_t cvh = tq::f32_to_f16(cv_e);
-        constexpr int NV = (1 << (2 * VB)) * QPE;
+        // entry e holds pair e mod 2^(2 VB) (byte windows: the byte's two spare bits ignored)
+        constexpr int NV = (Sm::VWIN ? 256 : (1 << (2 * VB))) * QPE;
         for (int i = tid; i < (NV + 63) / 64 * 64; i += NT / 2) {
             const int e = i / QPE, qd = i % QPE;
-            const uint32_t v = from_lane(cvh, e & ((1 << VB) - 1)) | (from_lane(cvh, e >> VB) << 16);
+            const int pr = e & ((1 << (2 * VB)) - 1);
+            const uint32_t v = from_lane(cvh, pr & ((1 << VB) - 1)) | (from_lane(cvh, pr >> VB) << 16);
             if (i < NV) tab4[e * 16 + qd] = make_uint4(v, v, v, v);
         }
         if constexpr (KI8) {
@@ -794,10 +817,11 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             const int ci = (int)rintf(ck_e * ldexpf(1.0f, E));
             const int l0 = ((ci + 128) & 255) - 128;
             const uint32_t limbs = (uint32_t)(l0 & 255) | ((uint32_t)(((ci - l0) >> 8) & 255) << 8);
-            constexpr int NK = (1 << (2 * KB)) * QPE;
+            constexpr int NK = (Sm::KWIN ? 256 : (1 << (2 * KB))) * QPE;
             for (int i = tid; i < (NK + 63) / 64 * 64; i += NT / 2) {
                 const int e = i / QPE, qd = i % QPE;
-                const uint32_t v = from_lane(limbs, e & ((1 << KB) - 1)) | (from_lane(limbs, e >> KB) << 16);
+                const int pr = e & ((1 << (2 * KB)) - 1);
+                const uint32_t v = from_lane(limbs, pr & ((1 << KB) - 1)) | (from_lane(limbs, pr >> KB) << 16);
                 if (i < NK) tab4[e * 16 + 8 + qd] = make_uint4(v, v, v, v);
             }
         } else {
@@ -858,6 +882,18 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
         for (int i = 0; i < R::HPL; ++i) sq[i] = qjl_combine<GC>(acc_all, i) * (0.5f * qfix);
     }
+    // T2 over the prologue's area, once every wave holds its operands: entry e = T0 entry e / 4
+    // (the pair in bits 2..7 of the byte)
+    if constexpr (Sm::WIN) {
+        __syncthreads();
+        const uint4* tab4 = reinterpret_cast<const uint4*>(&sm.tab[0][0]);
+        uint4* t24 = reinterpret_cast<uint4*>(&sm.u.t2[0][0]);
+        for (int i = tid; i < 256 * 16; i += NT) {
+            const int e = i >> 4, part = i & 15;  // parts 0..7 value copies, 8..15 int8 key copies
+            if (part < 8 ? Sm::VWIN : Sm::KWIN) t24[i] = tab4[(e >> 2) * 16 + part];
+        }
+        __syncthreads();
+    }
 
     // per-lane softmax state (heads of this lane group) and value accumulators.  The reference
     // maximum m_ref tracks max(score + e_v) - WEXP0, e_v = the biased f16 exponent of the value
@@ -877,6 +913,10 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     const uint32_t plane = 4u * (uint32_t)(lane & (TCOPIES - 1));        // value copy: +4 c
     const uint32_t kplane = KI8 ? 128u + plane : 8u * (uint32_t)(lane & (Sm::KC - 1));  // key copy
     constexpr int KSHIFT = KI8 ? 8 : (Sm::KC == 32 ? 8 : 7);  // log2 bytes per key-table entry row
+    // byte-window lookups: the copy offsets with byte 2 = 1 (T2 lies 64 KB above T0)
+    const uint32_t kwin = kplane | 0x10000u, vwin = plane | 0x10000u;
+    static_assert(!Sm::WIN || offsetof(Sm, u) == offsetof(Sm, tab) + 65536, "T2 = T0 + 64 KB");
+    const char* const tb0 = reinterpret_cast<const char*>(&sm) + offsetof(Sm, tab);
     // the weight of token n = 4 i + k lands in dword i of lane group k's slots
     const int wslot = 4 * (n & 3) + (n >> 2);
 
@@ -913,7 +953,18 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         }
         if constexpr (KI8) {
             // 4 int8 MFMAs per block, dims 32 g + 8 j + 2 i + e: one 4-byte lookup per pair of codes
-            // returns both codes' limbs in k-slot order
+            // returns both codes' limbs in k-slot order.  3-bit codes: pair 4 j + i at bit 6 (4 j +
+            // i) of the lane's 96 bits, a byte window of kw (bit 0 or 2 mod 8) or of kw >> 4 (4, 6)
+            uint32_t ksh[NB][3];
+            if constexpr (Sm::KWIN) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const Kd& B = kset[s0 + b];
+                    ksh[b][0] = __builtin_amdgcn_alignbit(B.kw[1], B.kw[0], 4);
+                    ksh[b][1] = __builtin_amdgcn_alignbit(B.kw[2], B.kw[1], 4);
+                    ksh[b][2] = B.kw[2] >> 4;
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -926,10 +977,12 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                         if constexpr (KB == 4) {
                             // code byte i of dword j: LDS byte offset 256 * byte + kplane in one v_perm
                             off = __builtin_amdgcn_perm(B.kw[j], kplane, 0x0C0C0000u | ((4u + (uint32_t)i) << 8));
+                        } else if constexpr (Sm::KWIN) {
+                            off = win_off(B.kw, ksh[b], KB * (8 * j + 2 * i), kwin);
                         } else {
                             off = field_x<2 * KB, 8>(B.kw, KB * (8 * j + 2 * i)) | kplane;
                         }
-                        bk[i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.tab) + off);
+                        bk[i] = *reinterpret_cast<const uint32_t*>(tb0 + off);
                     }
                     acc_i[b] = mfma_i8(qa[j], bk, acc_i[b]);
                 }
@@ -1075,10 +1128,15 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                     if constexpr (VB == 4) {
                         // code byte u: LDS byte offset 256 * byte + plane in one v_perm
                         off = __builtin_amdgcn_perm(ch[b][i], plane, 0x0C0C0000u | ((4u + (uint32_t)u) << 8));
+                    } else if constexpr (Sm::VWIN) {
+                        // pair u at bit 6 u of the chunk: byte windows of the chunk (u = 0, 3) or
+                        // of chunk >> 4 (u = 1, 2)
+                        const uint32_t chs = ch[b][i] >> 4;
+                        off = win_off(&ch[b][i], &chs, 6 * u, vwin);
                     } else {
                         off = field_x<2 * VB, 8>(&ch[b][i], 2 * VB * u) | plane;
                     }
-                    bv[i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(sm.tab) + off);
+                    bv[i] = *reinterpret_cast<const uint32_t*>(tb0 + off);
                 }
                 acc_v[b][u] = mfma_f16(av[b], bv, acc_v[b][u]);
             }
