@@ -777,7 +777,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8 codes; bf16 hi/lo + int8 MFMA, fp32 accumulate",
+        "dtype": ("u8 codes; int8-limb key MFMAs (<= 4 heads per KV head, else bf16 hi/lo), fp16 value "
+                  "MFMAs, fp32 accumulate"),
         "data": "synthetic",
         "config": {
             "workload": (f"{_shape_name(B, Hq, Hkv, N, bits, qjl)}: decode attention over {args.layers} "
