@@ -23,12 +23,15 @@ def u16(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def build_layer(cuda, B, Hkv, N, bits, qjl, seed, cap=None, kv_mu=None):
+def build_layer(cuda, B, Hkv, N, bits, qjl, seed, cap=None, kv_mu=None, v_mu=None, v_sigma=None):
     cap = cap or N
     lc = layer_codecs(D, bits, 0, qjl, cuda)
     kw = {} if kv_mu is None else {"mu": kv_mu}
+    vw = {} if v_mu is None else {"mu": v_mu}
+    if v_sigma is not None:
+        vw["sigma"] = v_sigma
     k = kv_bf16((B, Hkv, N, D), seed=seed, device=cuda, **kw)
-    v = kv_bf16((B, Hkv, N, D), seed=seed + 1, device=cuda)
+    v = kv_bf16((B, Hkv, N, D), seed=seed + 1, device=cuda, **vw)
     L = {
         "kcodes": torch.zeros(B, Hkv, cap, K.row_bytes(D, lc.key_bits), dtype=torch.uint8, device=cuda),
         "knorms": torch.zeros(B, Hkv, cap, dtype=torch.float16, device=cuda),
@@ -173,6 +176,22 @@ def test_attention_sharp_softmax(cuda):
     _, out32 = run(lc, L, q, 5000)
     torch.cuda.synchronize()
     check(out32, O.fused_attention_f64(u16(q), host_layer(lc, L, 5000)))
+
+
+@pytest.mark.parametrize("Hq,v_mu,v_sigma", [
+    (8, float(np.log(2e-3)), 0.3),   # tiny value norms (f16 exponents near the bottom of the range)
+    (8, float(np.log(4e3)), 0.3),    # large value norms
+    (8, float(np.log(20.0)), 2.0),   # norms spread over five decades within one sequence
+    (14, float(np.log(20.0)), 2.0),  # the same through the 5-8-head kernel
+])
+def test_attention_extreme_value_norms(cuda, Hq, v_mu, v_sigma):
+    """The fp16 value sum takes p |v| as an fp16 weight; the lazy maximum tracks the value norm's
+    exponent so that those weights neither overflow nor lose their leading bits."""
+    lc, L = build_layer(cuda, 1, 2, 3000, 4, True, seed=23, v_mu=v_mu, v_sigma=v_sigma)
+    q = query_bf16(1, Hq, D, seed=23, device=cuda)
+    _, out32 = run(lc, L, q, 3000)
+    torch.cuda.synchronize()
+    check(out32, O.fused_attention_f64(u16(q), host_layer(lc, L, 3000)))
 
 
 def test_attention_on_reference_golden_layer(cuda, golden_dir):

@@ -15,13 +15,17 @@
 //
 // Per 16-token block, lane l = (n = l & 15, g = l >> 4):
 //
-//   key score     v_mfma_f32_16x16x32_bf16, D[row][token] += A[row][k] B[k][token].
-//                 A (registers, fixed for the call): rows = (query head, hi|lo part of
-//                 q_rot = q R_k^T in bf16), k-slots = (dim, hi|lo part of the codebook
-//                 value); B = the dequantised keys, one 8-byte LDS lookup per pair of
-//                 codes returning (Ck_hi, Ck_lo) for both.  Every cross product of the
-//                 two-term splits is formed, so the score carries ~2^-17 relative error
-//                 against fp32 inputs (the tolerance is 2e-3 of |out|).
+//   key score     up to 4 query heads per KV head: v_mfma_i32_16x16x64_i8, 4 per block.
+//                 A (registers, fixed for the call): q_rot = q R_k^T times the logit scale
+//                 in fixed point, x = rint(q_rot 2^F) with |x| < 2^22, as three balanced
+//                 base-256 digits X0..X2; rows = (query head, s = 0..3), k-slots = (dim, key
+//                 limb m), row s holding digit X_(s-m).  B = the dequantised keys, Ck 2^E
+//                 (|.| < 2^15) as two int8 limbs L0 + 256 L1, one 4-byte LDS lookup per pair
+//                 of codes.  The score is (R0 + 256 R1) + 65536 (R2 + 256 R3) of the head's
+//                 four rows: both sums exact in int32, then one fp32 rounding.
+//                 5..8 heads: v_mfma_f32_16x16x32_bf16, 8 per block, rows = (head, hi|lo part
+//                 of q_rot in bf16), k-slots = (dim, hi|lo part of Ck), one 8-byte lookup per
+//                 pair of codes; every cross product of the two-term splits is formed.
 //   QJL term      v_mfma_i32_16x16x64_i8 on the sign bits left in place (one v_and per 4
 //                 dims: bit i of each byte is worth 2^i, -128 for i = 7) against q_proj =
 //                 q S^T in fixed point divided by the same 2^i, split in four int8 limbs
@@ -29,11 +33,17 @@
 //   softmax       online, base 2 (scores are pre-multiplied by log2 e), with a lazily
 //                 raised reference maximum: weights are exp2(score - m_ref) and m_ref
 //                 is raised (with a rescale of the partial sums) only when a score
-//                 exceeds it by more than 2^8, so blocks pay no cross-lane reduction.
-//   value sum     v_mfma_f32_16x16x32_bf16, D[(head, w hi|lo)][dim] += A B: A = the
-//                 softmax weights p |v| split hi/lo, transposed through LDS; B = value
-//                 codes dequantised by single-code LDS lookups (Cv_hi, Cv_lo) from a
-//                 table small enough to be bank-conflict free.
+//                 exceeds it by more than 2^8, so blocks pay no cross-lane reduction.  m_ref
+//                 also tracks the value norm's f16 exponent, which keeps the fp16 weights of
+//                 the value sum in range.
+//   value sum     v_mfma_f32_16x16x32_f16, 4 per block, D[(head, dim parity)][column] += A B:
+//                 A = the softmax weights p |v| in fp16, transposed through per-wave LDS rows;
+//                 B = the value codes dequantised in pairs, one 4-byte LDS lookup per pair
+//                 of codes returning (Cv[c0], Cv[c1]) in fp16.
+//   lookups       pair tables with 32 lane-private copies of every entry (a 32-lane LDS pass
+//                 never conflicts).  A pair of 4-bit codes is a byte of the packed words, a
+//                 pair of 3-bit codes a "byte window" (a byte holding the 6-bit field in bits
+//                 0..5, table T0, or 2..7, table T2): one v_perm forms each lookup address.
 //
 // All global reads are buffer loads against per-wave descriptors whose size is the
 // wave's token range: a lane offset fixed for the call plus a scalar block offset,
