@@ -42,8 +42,19 @@ def _at_slot(t: torch.Tensor | None, start: int):
     return None if t is None else ctypes.c_void_p(t.data_ptr() + start * t.stride(2) * t.element_size())
 
 
+#: the current stream's handle as an int: torch's raw accessor is one C call, where
+#: torch.cuda.current_stream() builds a Stream object (~2 us per call)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_handle(device: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def _stream(device: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    return ctypes.c_void_p(_stream_handle(device))
 
 
 def _require_gpu(*tensors: torch.Tensor | None) -> None:
@@ -255,7 +266,7 @@ def _workspace_for(device: torch.device, stream: int, batch: int, q_heads: int, 
 
 def attention_workspace(device: torch.device, batch: int, q_heads: int, kv_heads: int, max_tokens: int) -> torch.Tensor:
     """The partials workspace of ``tq_decode_attention`` for the current stream of ``device``."""
-    return _workspace_for(device, torch.cuda.current_stream(device).cuda_stream, batch, q_heads, kv_heads)
+    return _workspace_for(device, _stream_handle(device), batch, q_heads, kv_heads)
 
 
 def _ptr(t: torch.Tensor | None):
@@ -293,7 +304,7 @@ def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.T
     B, Hq, D = q.shape
     Hkv, cap = k_codes.shape[1], k_codes.shape[2]
     dev = q.device
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _stream_handle(dev)
     out_bf16 = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=dev)
     out_f32 = torch.empty((B, Hq, D), dtype=torch.float32, device=dev) if want_f32 else None
     lse = torch.empty((B, Hq), dtype=torch.float32, device=dev) if want_lse else None
