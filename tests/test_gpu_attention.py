@@ -122,6 +122,30 @@ def test_attention_capacity_and_seq_lens(cuda):
     check(out32, ref)
 
 
+@pytest.mark.parametrize("Hq,Hkv,bits,qjl", [(8, 2, 4, True), (10, 2, 3, False)])
+def test_attention_seq_starts_and_lens(cuda, Hq, Hkv, bits, qjl):
+    """Per-row attended ranges [seq_starts[b], seq_lens[b]) (what a left- or right-padded mask
+    becomes): starts and ends off the 16-token blocks, a range inside the last few of the
+    group's splits (every earlier split empty), a single token, start = end and start > end
+    (both empty: zero output), with real data in the slots outside every range and past
+    n_tokens.  Four and five query heads per KV head (the two split-kernel families)."""
+    B, N, cap = 6, 5000, 5200
+    lc, L = build_layer(cuda, B, Hkv, cap, bits, qjl, seed=909 + bits, cap=cap)
+    q = query_bf16(B, Hq, D, seed=91, device=cuda)
+    starts = np.array([0, 37, 4900, 1, 2500, 3000], dtype=np.int32)
+    lens = np.array([5000, 4999, 5000, 2, 2500, 2000], dtype=np.int32)
+    out16, out32 = K.decode_attention(q, k_codes=L["kcodes"], k_norms=L["knorms"], v_codes=L["vcodes"],
+                                      v_norms=L["vnorms"], n_tokens=N, key=lc.key, value=lc.value,
+                                      k_signs=L["signs"], k_rnorms=L["rnorms"], qjl=lc.qjl,
+                                      seq_lens=torch.from_numpy(lens), seq_starts=torch.from_numpy(starts),
+                                      want_f32=True)
+    torch.cuda.synchronize()
+    ref = O.fused_attention_f64(u16(q), host_layer(lc, L, N), n_valid=lens, n_start=starts)
+    assert np.all(out32[4:].cpu().numpy() == 0.0)  # empty ranges attend to nothing
+    check(out32, ref)
+    assert np.array_equal(u16(out16), O.f32_to_bf16_bits(out32.cpu().numpy()))
+
+
 def test_attention_empty_cache_is_zero(cuda):
     lc, L = build_layer(cuda, 1, 2, 4, 4, True, seed=1)
     q = query_bf16(1, 8, D, seed=1, device=cuda)
