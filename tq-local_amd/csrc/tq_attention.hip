@@ -276,7 +276,7 @@ struct Smem {
         uint32_t t2[WIN ? 256 : 1][64];                // T2, built over the prologue's area
         struct {
             uint4 img[IMG_DW / 4];      // this group's q-side image
-            uint4 qst[NW][NH * 16];     // per-wave copy of the group's query rows
+            uint4 qst[NW][NH * 16 > 128 ? NH * 16 : 128];  // per wave: the query rows, then the R_k / S restage
             PrepLds<GC> ps;             // scratch of the image builder
         } pro;
         struct {
@@ -418,12 +418,15 @@ __global__ __launch_bounds__(MT) void merge_kernel(const float* __restrict__ par
 // heads, bf16 as given, exact); B = the matrix rows, each fp32 element split exactly into three
 // bf16 terms hi + mid + lo (truncations: hi keeps the top 8 significant bits, mid the next 8,
 // and the rest has at most 8), so every product is exact and the sums are fp32 MFMA
-// accumulations.  Lane (c, kq) reads 32 bytes of each of rows 16 t + c per k-step: 16 rows per
-// load instruction instead of one row per lane.
+// accumulations.  Each load instruction reads whole 128-byte lines: the columns [32 s, 32 s +
+// 32) of 8 of the tile's rows, lane l row 8 hf + l / 8, floats 32 s + 4 (l mod 8) .. + 3.  The
+// wave restages each k-step's 2 KB through its own LDS slot into the MFMA layout (lane (c, kq):
+// row c, floats 32 s + 8 kq .. + 7).  Loads that instead took 64 bytes of each of 16 rows per
+// instruction (the MFMA layout directly) arrived about half as fast.
 
 // hi | mid | lo bf16 terms of the 8 floats of one lane's k-step (element e <-> k-slot e)
-__device__ __forceinline__ void split3_bf16(const float4& a, const float4& b, u32x4& hi, u32x4& mid, u32x4& lo) {
-    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+__device__ __forceinline__ void split3_bf16(const f32x4& a, const f32x4& b, u32x4& hi, u32x4& mid, u32x4& lo) {
+    const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         const uint32_t x0 = __float_as_uint(x[2 * p]), x1 = __float_as_uint(x[2 * p + 1]);
@@ -456,8 +459,8 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
     const int c = lane & 15, kq = lane >> 4;
     // A: lane (row c = query head, kq) holds q[c][32 s + 8 kq + e] for k-step s
     u32x4 qa[4];
-    // B: lane (column c, kq) holds row 16 t' + c, elements 32 s + 8 kq + e
-    float4 rr[TPW][8];
+    // B as loaded: rr[u][2 s + hf], lane l: row 16 t' + 8 hf + l / 8, floats 32 s + 4 (l mod 8) .. + 3
+    f32x4 rr[TPW][8];
     // the group's query rows, 16 bytes per lane (rows >= G read as zero through the descriptor),
     // restaged in the wave's LDS slot below: one load per NH / 4 rows instead of four per lane,
     // most of them repeats of the same rows
@@ -470,12 +473,12 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
         for (int u = 0; u < TPW; ++u) {
             const int t = wave + u * NW;
             if (t < NTILE) {
-                const float* row = (t < 8 ? Rk : S) + (size_t)(16 * (t & 7) + c) * D + 8 * kq;
+                const float* row = (t < 8 ? Rk : S) + (size_t)(16 * (t & 7) + (lane >> 3)) * D + 4 * (lane & 7);
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    rr[u][2 * s] = *reinterpret_cast<const float4*>(row + 32 * s);
-                    rr[u][2 * s + 1] = *reinterpret_cast<const float4*>(row + 32 * s + 4);
-                }
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf)
+                        rr[u][2 * s + hf] = *reinterpret_cast<const f32x4*>(row + (size_t)(8 * hf) * D + 32 * s);
             }
         }
     }
@@ -495,6 +498,11 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
 #pragma unroll
         for (int s = 0; s < 4; ++s) qa[s] = u32x4{0u, 0u, 0u, 0u};
     }
+    // the same slot restages the matrix rows (2 KB per k-step; the qa reads above come first in
+    // the wave's LDS order): lane (c, kq) takes row c's floats 32 s + 8 kq .. + 7, which lanes
+    // 8 (c mod 8) + 2 kq and + 1 of instruction c / 8 loaded
+    f32x4* const rst = reinterpret_cast<f32x4*>(qst);
+    const int src = 64 * (c >> 3) + 8 * (c & 7) + 2 * kq;
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
         const int t = wave + u * NW;
@@ -502,8 +510,11 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
+            rst[lane] = rr[u][2 * s];
+            rst[64 + lane] = rr[u][2 * s + 1];
+            const f32x4 b0 = rst[src], b1 = rst[src + 1];
             u32x4 hi, mid, lo;
-            split3_bf16(rr[u][2 * s], rr[u][2 * s + 1], hi, mid, lo);
+            split3_bf16(b0, b1, hi, mid, lo);
             acc = mfma_bf16(qa[s], lo, acc);
             acc = mfma_bf16(qa[s], mid, acc);
             acc = mfma_bf16(qa[s], hi, acc);
