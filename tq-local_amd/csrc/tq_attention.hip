@@ -87,6 +87,11 @@ struct Cfg {
     static constexpr int NSET = GC == 1 ? TQ_ATTN_SETS_G4 : TQ_ATTN_SETS_G8;
     // blocks a wave takes through every stage together (NSET is a multiple)
     static constexpr int NB = GC == 1 ? TQ_ATTN_NB_G4 : TQ_ATTN_NB_G8;
+    // register sets of token blocks loaded before the q-side products (the rest right after
+    // them): every load instruction issued ahead of a wave's R_k / S rows delays them, and the
+    // younger waves' rows wait behind the older waves' token loads.  With 5-8 heads the products
+    // take longer (two tiles on some waves), so one set goes first.
+    static constexpr int PRO_SETS = GC == 1 ? 0 : 1;
 };
 constexpr int BLK = 16;        // tokens per block (MFMA N)
 constexpr float NEG_INF = -__builtin_huge_valf();
@@ -791,11 +796,11 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // computes them: the mat-vecs on the matrix cores from L2-resident R_k and S, cheaper than
     // a separate launch ahead of the split pass)
     uint32_t* img = reinterpret_cast<uint32_t*>(sm.u.pro.img);
-    // every global load of the prologue is issued before any is waited for: the codebook entries
-    // (unconditionally, in range), the products' operands, then the first blocks of the token
-    // loop, whose HBM latency the rest of the prologue covers
-    const float ck_e = Ck[tid & ((1 << KB) - 1)];
-    const float cv_e = Cv[tid & ((1 << VB) - 1)];
+    // the products' operands are loaded first, then the codebook entries (unconditionally, in
+    // range; only the tables below use them) and the first blocks of the token loop
+    // (PRO_SETS register sets before the products, the rest after them), whose HBM latency the
+    // rest of the prologue covers
+    float ck_e, cv_e;
     // int8 keys: the key codebook in fixed point, |Ck| 2^E < 2^15 (wave-uniform scalar loads)
     int E = 0;
     if constexpr (KI8) {
@@ -806,13 +811,21 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         if (cmax > 0.0f) (void)frexpf(cmax, &e);  // cmax < 2^e
         E = 15 - e;
     }
+    constexpr int PRO_SETS = Cfg<VB, GC, QJL>::PRO_SETS;
     image_products<QJL, GC, NW, KI8>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, sm.u.pro.qst[wave], wave, lane, [&] {
+        ck_e = Ck[tid & ((1 << KB) - 1)];
+        cv_e = Cv[tid & ((1 << VB) - 1)];
 #pragma unroll
-        for (int s = 0; s < NSET; ++s) {
+        for (int s = 0; s < PRO_SETS; ++s) {
             load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
             __builtin_amdgcn_sched_barrier(0);
         }
     });
+#pragma unroll
+    for (int s = PRO_SETS; s < NSET; ++s) {
+        load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // pair tables from the codebook entries in the lanes (lane l holds Ck[l mod 2^KB] and
     // Cv[l mod 2^VB]; ds_bpermute), four copies of an entry per 16-byte write, by the older half
     // of the waves: they finish their products first and wait at the barrier below for the
