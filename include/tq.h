@@ -104,6 +104,10 @@ size_t tq_decode_attention_workspace_bytes(int batch, int q_heads, int kv_heads,
  *            ordered on one stream)
  * logit_t = scale * (|k_t| <q R_k^T, C_k[kidx_t]> + sqrt(pi/2)/D |r_t| <q S^T, s_t>)
  * out     = (sum_t softmax_t |v_t| C_v[vidx_t]) @ R_v
+ * The value sums run on fp16 matrix cores: each value centroid enters as its fp16
+ * rounding (nearest even).  Over long, evenly spread softmaxes those rounding errors add
+ * up; pass value_centers through tq_value_codebook_f16 (below) once per codebook to keep
+ * them from doing so.
  */
 int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads, int dim,
                         const int32_t* seq_starts, const int32_t* seq_lens, int64_t n_tokens, int64_t cap,
@@ -115,6 +119,21 @@ int tq_decode_attention(const uint16_t* q, int batch, int q_heads, int kv_heads,
                         const float* value_rotation, const float* value_centers,
                         float scale, float* out_f32, uint16_t* out_bf16, float* lse_out,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The fp16 form of a value codebook for tq_decode_attention.  Host memory in and out;
+ * no GPU.  No counterpart in the reference, whose kernel reads the fp32 centroids
+ * (runtime/triton_kernels.py:187): it is for callers
+ * of tq_decode_attention, which rounds value_centers to fp16.  Each centroid is given one
+ * of its two fp16 neighbours, the combination that minimises |sum_c P_c (out_c - c)|, P_c
+ * the probability of code c under the coordinate density the Lloyd-Max codebook is built
+ * for, (1 - x^2)^((dim - 3)/2) on [-1, 1], cells split at the centroids' midpoints.  The
+ * output values are exactly representable in fp16.
+ *   centers  fp32 [2^bits], strictly increasing, |c| < 1 (host)
+ *   bits     1..4;  dim >= 3 (the head dimension the codebook was built for)
+ *   out      fp32 [2^bits] (host)
+ */
+int tq_value_codebook_f16(const float* centers, int bits, int dim, float* out);
 
 /*
  * tq_decode_attention without a workspace argument and without any allocation.

@@ -146,6 +146,31 @@ def test_attention_seq_starts_and_lens(cuda, Hq, Hkv, bits, qjl):
     assert np.array_equal(u16(out16), O.f32_to_bf16_bits(out32.cpu().numpy()))
 
 
+@pytest.mark.parametrize("bits,qjl", [(4, True), (3, False)])
+def test_attention_diffuse_softmax_long_context(cuda, bits, qjl):
+    """An evenly spread softmax over 131,072 tokens (queries scaled by 1e-3): the output is a
+    near-cancelling average of the values, where a value centroid's fp16 rounding error,
+    the same for every token that carries the code, would add up (as sqrt(tokens) against
+    the output).  The kernel is given the balanced fp16 codebook (tq_value_codebook_f16);
+    the nearest-even codebook's error on the same inputs is printed beside it."""
+    from dataclasses import replace
+
+    B, Hq, Hkv, N = 1, 8, 2, 131072
+    lc, L = build_layer(cuda, B, Hkv, N, bits, qjl, seed=4242 + bits)
+    q = (query_bf16(B, Hq, D, seed=77, device=cuda).float() * 1e-3).to(torch.bfloat16)
+    _, out32 = run(lc, L, q, N)
+    nearest = replace(lc.value, attn_centers=lc.value.centers)  # rounded to fp16 in the kernel
+    _, out_rne = K.decode_attention(q, k_codes=L["kcodes"], k_norms=L["knorms"], v_codes=L["vcodes"],
+                                    v_norms=L["vnorms"], n_tokens=N, key=lc.key, value=nearest,
+                                    k_signs=L["signs"], k_rnorms=L["rnorms"], qjl=lc.qjl, want_f32=True)
+    torch.cuda.synchronize()
+    ref = O.fused_attention_f64(u16(q), host_layer(lc, L, N))
+    inf = np.abs(ref).max()
+    err_rne = np.abs(out_rne.cpu().numpy().astype(np.float64) - ref).max() / inf
+    err = check(out32, ref)
+    print(f"[diffuse] bits {bits}: balanced codebook {err:.2e}, nearest-even {err_rne:.2e} of |out|_inf")
+
+
 def test_attention_empty_cache_is_zero(cuda):
     lc, L = build_layer(cuda, 1, 2, 4, 4, True, seed=1)
     q = query_bf16(1, 8, D, seed=1, device=cuda)

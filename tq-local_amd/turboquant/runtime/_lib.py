@@ -36,6 +36,7 @@ SIGNATURES: dict[str, tuple] = {
                                          _I, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P]),
     "tq_dequantize_mse": (_I, [_P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "tq_dequantize_prod": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _P]),
+    "tq_value_codebook_f16": (_I, [_P, _I, _I, _P]),
     "tq_group_matrix": (_I, [_P, _I, _P, _I, _P]),
     "tq_decode_attention_groups": (_I, [_P, _I, _I, _I, _I, _P, _P, _I64, _I64, _I, _P, _P, _P, _I, _P, _P, _P, _P,
                                         _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _SZ, _P]),

@@ -71,12 +71,17 @@ def row_bytes(dim: int, bits: int) -> int:
 
 @dataclass
 class CodecParams:
-    """Device-resident parameters of one Q_mse codec (rotation, codebook)."""
+    """Device-resident parameters of one Q_mse codec (rotation, codebook).
+
+    ``attn_centers`` caches the codebook's fp16 form for the decode attention's value sums
+    (``attention_value_centers``).
+    """
 
     bits: int
     rotation: torch.Tensor  # fp32 [D, D]
     centers: torch.Tensor  # fp32 [2^bits]
     boundaries: torch.Tensor  # fp32 [2^bits - 1]
+    attn_centers: torch.Tensor | None = None  # fp32 [2^bits], fp16-exact values
 
 
 @dataclass
@@ -273,6 +278,27 @@ def _ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+def value_codebook_f16(centers: np.ndarray, bits: int, dim: int = HEAD_DIM) -> np.ndarray:
+    """The fp16 value codebook of tq_decode_attention (host; tq_value_codebook_f16): each
+    centroid's fp16 neighbour below or above, chosen so that the rounding errors cancel
+    over the codes' probabilities instead of adding up over long contexts."""
+    c = np.ascontiguousarray(centers, dtype=np.float32)
+    if c.shape != (1 << bits,):
+        raise ValueError(f"expected {1 << bits} centers for {bits} bits, got {c.shape}")
+    out = np.empty_like(c)
+    _lib.call("tq_value_codebook_f16", c.ctypes.data, bits, dim, out.ctypes.data)
+    return out
+
+
+def attention_value_centers(codec: CodecParams) -> torch.Tensor:
+    """The value codebook tq_decode_attention is given: ``value_codebook_f16`` of the
+    codec's centers, on the codec's device, computed once per codec."""
+    if codec.attn_centers is None:
+        host = value_codebook_f16(codec.centers.detach().cpu().numpy(), codec.bits)
+        codec.attn_centers = torch.from_numpy(host).to(codec.centers.device)
+    return codec.attn_centers
+
+
 def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.Tensor, v_codes: torch.Tensor,
                      v_norms: torch.Tensor, n_tokens: int, key: CodecParams, value: CodecParams,
                      k_signs: torch.Tensor | None = None, k_rnorms: torch.Tensor | None = None,
@@ -320,7 +346,7 @@ def decode_attention(q: torch.Tensor, *, k_codes: torch.Tensor, k_norms: torch.T
     st = fn(q.data_ptr(), B, Hq, Hkv, D, _ptr(seq_starts), _ptr(seq_lens), int(n_tokens), cap,
             k_codes.data_ptr(), k_norms.data_ptr(), _ptr(k_signs), _ptr(k_rnorms), v_codes.data_ptr(),
             v_norms.data_ptr(), key.bits, value.bits, int(k_signs is not None), key.rotation.data_ptr(),
-            key.centers.data_ptr(), _ptr(qjl), value.rotation.data_ptr(), value.centers.data_ptr(), s,
+            key.centers.data_ptr(), _ptr(qjl), value.rotation.data_ptr(), attention_value_centers(value).data_ptr(), s,
             _ptr(out_f32), out_bf16.data_ptr(), _ptr(lse), ws.data_ptr(), ws.numel(), stream)
     if st != _lib.TQ_OK:
         _lib.check("tq_decode_attention", st)
