@@ -184,8 +184,10 @@ def bench_split(args, dev) -> dict:
     avg_us = e0.elapsed_time(e1) * 1e3 / (args.steps * args.layers)
     layer_bytes = int(layers[0].storage_bytes())
     achieved = layer_bytes / (avg_us * 1e-6) / 1e9
+    # at most 4 heads per KV head and 8 outlier channels: the split kernel's matrix-core path
+    mfma = Hq // Hkv <= 4 and args.outliers <= 8
     return {
-        "metric": "outlier-split decode-attn us/layer (channel-group kernel), 8B KV shape @32K",
+        "metric": "outlier-split decode-attn us/layer, 8B KV shape @32K",
         "value": round(avg_us, 1),
         "unit": "us/layer",
         "n_gpus": 1,
@@ -195,7 +197,7 @@ def bench_split(args, dev) -> dict:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8 codes; fp32 VALU",
+        "dtype": "u8 codes; int8/fp16 MFMA (normal group), fp32 (outlier group)" if mfma else "u8 codes; fp32 VALU",
         "data": "synthetic",
         "config": {
             "workload": (f"outlier split, {args.outliers} channels: {args.layers} layers, B={B}, Hq={Hq}, Hkv={Hkv}, "
@@ -206,7 +208,8 @@ def bench_split(args, dev) -> dict:
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "tq_decode_attention_groups = group_attn_kernel + merge_kernel, eager calls"},
+                     "kernel": "tq_decode_attention_groups = " + ("split_kernel (two groups)" if mfma else "group_attn_kernel")
+                     + " + merge_kernel, eager calls"},
         "prefill_quantizer": {"ms_per_layer": round(statistics.median(q_ms), 3)},
     }
 

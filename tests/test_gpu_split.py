@@ -420,6 +420,83 @@ def test_group_attention_shapes(cuda, Hq, Hkv, bits, extra, k, qjl):
     assert err <= TOL, err
 
 
+def _rows_range(groups: list[dict], b: int, start: int, end: int) -> list[dict]:
+    """Batch row b, tokens [start, end) of the oracle's per-group views."""
+    out = []
+    for g in groups:
+        h = dict(g)
+        for name in ("kcodes", "knorms", "vcodes", "vnorms", "signs", "rnorms"):
+            if h[name] is not None:
+                h[name] = h[name][b:b + 1, :, start:end]
+        out.append(h)
+    return out
+
+
+@pytest.mark.parametrize("bits,qjl,k,extra,Hq,Hkv", [
+    (4, True, 4, 1, 8, 2),    # the split of the headline configuration (GQA 4, 124 + 4 channels)
+    (4, True, 8, 1, 6, 2),    # 8 outlier channels, GQA 3
+    (3, True, 5, 2, 4, 4),    # 3-bit Q_prod (2-bit keys, 3-bit values), one head per KV head
+    (2, True, 3, 3, 4, 2),    # the smallest group (3 channels)
+    (4, False, 3, 4, 8, 2),   # 8-bit outlier codes
+    (3, False, 7, 1, 8, 2),
+    (2, False, 3, 2, 4, 1),
+    (1, False, 6, 3, 12, 3),
+])
+def test_split_layer_matrix_core_attention(cuda, bits, qjl, k, extra, Hq, Hkv):
+    """Two-group layers with at most 4 query heads per KV head and at most 8 outlier
+    channels run on the matrix-core split kernel (group 0's rows at any byte alignment,
+    group 1 per lane): fp32 output against the fp64 formula over the groups at 2e-3, over
+    the whole range and over per-row ranges (a 1-token row, an offset start)."""
+    B, N = 3, 1237
+    kx = kv_bf16((B, Hkv, N, D), seed=70 + k, device=cuda, outlier_channels=k)
+    vx = kv_bf16((B, Hkv, N, D), seed=71 + k, device=cuda)
+    layer = PackedMSELayer(bits=bits, num_outlier_channels=k, outlier_extra_bits=extra, use_qjl_keys=qjl,
+                           quantize_decode=True)
+    layer.initialize_from_dense(kx, vx)
+    sc = layer._split
+    q = query_bf16(B, Hq, D, seed=72 + bits, device=cuda)
+    host = _host_groups(layer)
+    kw = dict(key_stack=sc.key_stack, value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, want_f32=True)
+    _, out = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=N, **kw)
+    ref = O.split_fused_attention_f64(u16(q), host, D)
+    err = np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max()
+    print(f"[split-mfma] bits {bits} qjl {qjl} k {k} extra {extra} G {Hq // Hkv}: whole range {err:.2e}", flush=True)
+    assert err <= TOL, err
+    starts, ends = [0, 5, 301], [N, 1000, 302]
+    _, out = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=N,
+                                       seq_starts=torch.tensor(starts, dtype=torch.int32),
+                                       seq_lens=torch.tensor(ends, dtype=torch.int32), **kw)
+    out = out.cpu().numpy()
+    for b in range(B):
+        ref = O.split_fused_attention_f64(u16(q)[b:b + 1], _rows_range(host, b, starts[b], ends[b]), D)[0]
+        err = np.abs(out[b] - ref).max() / np.abs(ref).max()
+        assert err <= TOL, (b, err)
+
+
+def test_split_full_size_c2_layer_attention(cuda):
+    """The headline configuration (B=8, Hq=32, Hkv=8, N=32768, 4-bit Q_prod) split 124 + 4
+    channels, at the split kernel's full launch geometry: batch rows 0 and 7 against the fp64
+    formula over the groups at 2e-3, and the bf16 output the RNE rounding of the fp32 one."""
+    B, Hq, Hkv, N = 8, 32, 8, 32768
+    kx = kv_bf16((B, Hkv, N, D), seed=2026, device=cuda, outlier_channels=4)
+    vx = kv_bf16((B, Hkv, N, D), seed=2027, device=cuda)
+    layer = PackedMSELayer(bits=4, num_outlier_channels=4, use_qjl_keys=True, quantize_decode=True)
+    layer.initialize_from_dense(kx, vx)
+    del kx, vx
+    sc = layer._split
+    q = query_bf16(B, Hq, D, seed=2028, device=cuda)
+    ob, of = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=N, key_stack=sc.key_stack,
+                                       value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, want_f32=True)
+    of = of.cpu().numpy()
+    assert np.array_equal(u16(ob), O.f32_to_bf16_bits(of))
+    host = _host_groups(layer)
+    for b in (0, 7):
+        ref = O.split_fused_attention_f64(u16(q)[b:b + 1], _rows_range(host, b, 0, N), D)[0]
+        err = np.abs(of[b] - ref).max() / np.abs(ref).max()
+        print(f"[split-mfma] C2 split layer, row {b}: {err:.2e}", flush=True)
+        assert err <= TOL, (b, err)
+
+
 @pytest.mark.parametrize("bits,qjl", [(5, False), (8, False), (6, True)])
 def test_single_group_attention_at_wide_bit_widths(cuda, bits, qjl):
     """One group of all 128 channels (n_groups = 1): the unsplit layer at widths the MFMA

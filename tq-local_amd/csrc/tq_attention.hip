@@ -79,9 +79,14 @@ constexpr int D = TQ_DIM;
 #ifndef TQ_ATTN_SETS_G8
 #define TQ_ATTN_SETS_G8 2
 #endif
-template <int VB, int GC, bool QJL>
+// layers quantized in two channel groups (SPL): the outlier group's registers take the
+// kernel past 128 VGPRs
+#ifndef TQ_ATTN_WAVES_SPL
+#define TQ_ATTN_WAVES_SPL 12
+#endif
+template <int VB, int GC, bool QJL, bool SPL = false>
 struct Cfg {
-    static constexpr int NW = GC == 1 ? TQ_ATTN_WAVES_G4 : TQ_ATTN_WAVES_G8;
+    static constexpr int NW = SPL ? TQ_ATTN_WAVES_SPL : (GC == 1 ? TQ_ATTN_WAVES_G4 : TQ_ATTN_WAVES_G8);
     static constexpr int NT = NW * 64;
     // per-wave blocks in flight (register sets of packed data)
     static constexpr int NSET = GC == 1 ? TQ_ATTN_SETS_G4 : TQ_ATTN_SETS_G8;
@@ -259,10 +264,21 @@ struct PrepLds {
     float red[16];                    // max |.| per matrix-core tile: R_k tiles 0..7, S tiles 8..15
 };
 
-template <int KB, int VB, bool QJL, int GC>
+// The outlier group of a two-group layer (SPL): at most OD1 channels, handled per lane in fp32
+constexpr int OD1 = 8;
+template <bool SPL>
+struct OutLds {
+    float q1[4][2][OD1];  // per query head: q_rot (log2 units) and q_proj (times the QJL scale) of the group's dims
+    float ck[256];        // the group's key and value codebooks (up to 8 bits)
+    float cv[256];
+};
+template <>
+struct OutLds<false> {};
+
+template <int KB, int VB, bool QJL, int GC, bool SPL = false>
 struct Smem {
     static constexpr int NH = 4 * GC;
-    static constexpr int NW = Cfg<VB, GC, QJL>::NW;
+    static constexpr int NW = Cfg<VB, GC, QJL, SPL>::NW;
     static constexpr bool KI8 = GC == 1;
     // Byte windows (3-bit codes): the 6-bit field of a code pair is looked up by a byte of the
     // packed words that holds it, one v_perm per lookup.  T0 (the pair tables) is indexed by a
@@ -290,7 +306,8 @@ struct Smem {
             float s[NW][NH];
         } epi;
     } u;
-    uint32_t wt[NW][Cfg<VB, GC, QJL>::NB][16][WROW];   // per-wave transposes of the softmax weights
+    uint32_t wt[NW][Cfg<VB, GC, QJL, SPL>::NB][16][WROW];   // per-wave transposes of the softmax weights
+    OutLds<SPL> ol;
 };
 
 // LDS byte offset (from T0's base) of the table entry of the 6-bit field at bit p of the word
@@ -567,9 +584,10 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
 }
 
 // Phase 2 (after a barrier): the QJL fixed-point exponent G2 (max |q_proj| 2^(G2 - 7) < 2^22,
-// G2 - 7 capped at 60) and the limb image.  Returns G2 in every thread.
+// G2 - 7 capped at 60) and the limb image of dims d < d0 (zero beyond: the outlier group of a
+// two-group layer has its own term).  Returns G2 in every thread.
 template <int GC, int NT>
-__device__ __forceinline__ int qjl_image(const PrepLds<GC>& L, uint32_t* img, int tid) {
+__device__ __forceinline__ int qjl_image(const PrepLds<GC>& L, uint32_t* img, int tid, int d0) {
     constexpr int NH = 4 * GC;
     float mx = 0.0f;
 #pragma unroll
@@ -582,7 +600,7 @@ __device__ __forceinline__ int qjl_image(const PrepLds<GC>& L, uint32_t* img, in
     uint8_t* ib = reinterpret_cast<uint8_t*>(img + IMG_QJ);
     for (int i = tid; i < NH * D; i += NT) {
         const int h = i / D, d = i % D, bit = d & 7;
-        int x = (int)rintf(L.qp[h][d] * ldexpf(1.0f, G2 - bit));
+        int x = d < d0 ? (int)rintf(L.qp[h][d] * ldexpf(1.0f, G2 - bit)) : 0;
         if (bit == 7) x = -x;  // bit 7 of a sign byte is worth -128
         const int gq = d >> 5, jj = bit >> 2, v = bit & 3, e8 = (d >> 3) & 3;
 #pragma unroll
@@ -618,9 +636,10 @@ __device__ __forceinline__ float qjl_combine(const i32x4 (&acc)[GC], int i) {
 // capped at 60), in three balanced base-256 digits X0..X2.  Key MFMA j, lane (row 4 h + s,
 // group g), byte 4 i + 2 e + m <-> dim d = 32 g + 8 j + 2 i + e and codebook limb m: the A operand
 // is X_{s-m}[h][d] where 0 <= s - m <= 2 and zero otherwise, so row 4 h + s sums the products of
-// digit pairs of weight 2^(8 s).  Returns F in every thread.
+// digit pairs of weight 2^(8 s).  Dims d >= d0 are zero (the outlier group of a two-group
+// layer).  Returns F in every thread.
 template <int NT>
-__device__ __forceinline__ int key_image_i8(const PrepLds<1>& L, uint32_t* img, int tid) {
+__device__ __forceinline__ int key_image_i8(const PrepLds<1>& L, uint32_t* img, int tid, int d0) {
     float mx = 0.0f;
 #pragma unroll
     for (int w = 0; w < 8; ++w) mx = fmaxf(mx, L.red[w]);
@@ -632,7 +651,7 @@ __device__ __forceinline__ int key_image_i8(const PrepLds<1>& L, uint32_t* img, 
     uint8_t* ib = reinterpret_cast<uint8_t*>(img + IMG_QA);
     for (int i = tid; i < 4 * D; i += NT) {
         const int h = i / D, d = i % D;
-        int x = (int)rintf(L.qr[h][d] * sc);
+        int x = d < d0 ? (int)rintf(L.qr[h][d] * sc) : 0;
         int X[3];
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
@@ -652,20 +671,40 @@ __device__ __forceinline__ int key_image_i8(const PrepLds<1>& L, uint32_t* img, 
     return F;
 }
 
-template <int KB, int VB, bool QJL, int GC>
-__global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
+// Layers quantized in two channel groups (the outlier split, reference
+// runtime/packed_qmse_cache.py:437-515), for the split kernel with OD > 0: group 0 (d0 = D - d1
+// channels, rotated dims 0 .. d0 - 1 of the stacked matrices) runs through the MFMA stages,
+// its rows of ceil(d0 b / 8) bytes read at any byte alignment (the q-side image is zero on
+// dims >= d0, so the bytes there, which belong to the next row, add nothing); group 1 (d1 <= OD
+// channels, dims d0 .. D - 1) adds a per-lane fp32 term to the scores and keeps its own value
+// sums, which replace dims d0 .. D - 1 of the MFMA sums at the end.
+struct Og {
+    int d0, d1;         // channels of the two groups
+    int r0k, r0s, r0v;  // group 0 row bytes: key codes, sign bits, value codes
+    int r1k, r1s, r1v;  // group 1 row bytes
+    int b1k, b1v;       // group 1 code widths (1..8)
+    const uint8_t *kc1, *ks1, *vc1;
+    const uint16_t *kn1, *kr1, *vn1;
+    const float *Ck1, *Cv1;
+    float cq1;          // the logit scale (log2 units) times sqrt(pi/2) / d1
+};
+
+template <int KB, int VB, bool QJL, int GC, int OD = 0>
+__global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
     const uint16_t* __restrict__ kn, const uint8_t* __restrict__ ks, const uint16_t* __restrict__ kr,
     const uint8_t* __restrict__ vc, const uint16_t* __restrict__ vn, const float* __restrict__ Rk,
     const float* __restrict__ S, float c_mse, float c_qjl,
     const float* __restrict__ Ck, const float* __restrict__ Cv, float scale,
-    int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml) {
-    using Sm = Smem<KB, VB, QJL, GC>;
+    int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml, Og og) {
+    constexpr bool SPL = OD > 0;
+    static_assert(!SPL || (GC == 1 && OD <= OD1), "two-group layers: at most 4 heads per KV head, OD <= OD1");
+    using Sm = Smem<KB, VB, QJL, GC, SPL>;
     using R = Rows<GC>;
     constexpr bool KI8 = Sm::KI8;
-    constexpr int NW = Cfg<VB, GC, QJL>::NW;
-    constexpr int NT = Cfg<VB, GC, QJL>::NT;
+    constexpr int NW = Cfg<VB, GC, QJL, SPL>::NW;
+    constexpr int NT = Cfg<VB, GC, QJL, SPL>::NT;
     constexpr int KROW = D * KB / 8;  // bytes per key row
     constexpr int VROW = D * VB / 8;  // bytes per value row
     constexpr int VCH = 8 * VB;       // bits of one lane's 8-dim value chunk
@@ -706,45 +745,124 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     constexpr int STEP = NW * BLK;
     const size_t row0 = (size_t)grp * cap + (size_t)(t0 < n_tokens ? t0 : 0);
 
-    // workgroup buffer descriptors over [t0, t1): reads beyond the range return 0
-    const __amdgpu_buffer_rsrc_t rk = rsrc(kc + row0 * KROW, ntok * KROW);
-    const __amdgpu_buffer_rsrc_t rv = rsrc(vc + row0 * VROW, ntok * VROW);
+    // row bytes: the full-width rows, or group 0's of a two-group layer
+    const int krow = SPL ? og.r0k : KROW, srow = SPL ? og.r0s : D / 8, vrow = SPL ? og.r0v : VROW;
+    // workgroup buffer descriptors over [t0, t1): reads beyond the range return 0.  A row array
+    // of a two-group layer starts at any byte: its descriptor starts at the dword holding the
+    // range's first byte (*A = that byte's offset in it) and ends at a dword boundary.  The
+    // bytes past the range that the last dword holds lie in the page of the range's last byte
+    // (an aligned dword never crosses a page), and no valid token's code comes from them.
+    const auto rs_row = [&](const void* arr, int r, int* A) {
+        const size_t b0 = row0 * (size_t)r;
+        *A = SPL ? (int)(b0 & 3) : 0;
+        return rsrc(static_cast<const uint8_t*>(arr) + (b0 - (size_t)*A), ((int64_t)*A + ntok * r + 3) & ~(int64_t)3);
+    };
+    int Ak = 0, As = 0, Av = 0;
+    const __amdgpu_buffer_rsrc_t rk = rs_row(kc, krow, &Ak);
+    const __amdgpu_buffer_rsrc_t rv = rs_row(vc, vrow, &Av);
     const __amdgpu_buffer_rsrc_t rkn = rsrc(kn + row0, ntok * 2);
     const __amdgpu_buffer_rsrc_t rvn = rsrc(vn + row0, ntok * 2);
     __amdgpu_buffer_rsrc_t rs = rkn, rkr = rkn;
     if constexpr (QJL) {
-        rs = rsrc(ks + row0 * (D / 8), ntok * (D / 8));
+        rs = rs_row(ks, srow, &As);
         rkr = rsrc(kr + row0, ntok * 2);
     }
 
-    // lane offsets (bytes) into the per-wave buffers
-    const int ko = n * KROW + 4 * KB * g;        // key codes of token n, dims [32 g, 32 g + 32)
-    const int so = n * (D / 8) + 4 * g;          // sign bits of token n, same dims
-    const int no = 2 * n;                        // f16 norms of token n
-    const int vbit0 = VCH * n;                   // value chunk of lane n: dims [8 n, 8 n + 8)
-    // the dword holding the chunk's first bit, and the chunk's offset in it.  A 3-bit chunk (24
-    // bits at 24 n) straddles two dwords only for n = 1, 2 mod 4 (offsets 24, 16), and then its
-    // second dword is the first dword of lane n + 1's chunk: each lane reads one dword per row
-    // and takes the next one from its neighbour (reading both dwords in every lane made the
-    // value stream ~16% slower to load)
-    const int vdw = vbit0 >> 5;
-    const int vo = 4 * vdw + g * VROW;           // + 4 r VROW for token 4 r + g (each load: 4 whole rows)
-    const int vsh = vbit0 - 32 * vdw;            // in [0, 32)
+    // lane offsets (bytes) into the per-wave buffers.  Rows at any byte alignment (two-group
+    // layers) are read from the dword holding the lane's first byte and realigned by a bit
+    // shift fixed for the call (block offsets are multiples of 16 rows, so of 4 bytes)
+    const int kraw = Ak + n * krow + 4 * KB * g;  // key codes of token n, dims [32 g, 32 g + 32)
+    const int ko = kraw & ~3, kalign = 8 * (kraw & 3);
+    const int sraw = As + n * srow + 4 * g;       // sign bits of token n, same dims
+    const int so = sraw & ~3, salign = 8 * (sraw & 3);
+    const int no = 2 * n;                         // f16 norms of token n
+    int vo, vsh;
+    if constexpr (SPL) {
+        // lane n's chunk (dims [8 n, 8 n + 8), VB bytes) in the row of token g; + 4 r vrow for
+        // token 4 r + g.  Two dwords per row, realigned by vsh
+        const int vraw = Av + g * vrow + VB * n;
+        vo = vraw & ~3;
+        vsh = 8 * (vraw & 3);
+    } else {
+        // the dword holding the chunk's first bit, and the chunk's offset in it.  A 3-bit chunk
+        // (24 bits at 24 n) straddles two dwords only for n = 1, 2 mod 4 (offsets 24, 16), and
+        // then its second dword is the first dword of lane n + 1's chunk: each lane reads one
+        // dword per row and takes the next one from its neighbour (reading both dwords in every
+        // lane made the value stream ~16% slower to load)
+        const int vbit0 = VCH * n;                // value chunk of lane n: dims [8 n, 8 n + 8)
+        const int vdw = vbit0 >> 5;
+        vo = 4 * vdw + g * VROW;                  // + 4 r VROW for token 4 r + g (each load: 4 whole rows)
+        vsh = vbit0 - 32 * vdw;                   // in [0, 32)
+    }
+    // group 1 of a two-group layer: token n's rows (at most 8 bytes each) from the dword
+    // holding their first byte, and its three norms
+    __amdgpu_buffer_rsrc_t rk1 = rkn, rs1 = rkn, rv1 = rkn, rkn1 = rkn, rkr1 = rkn, rvn1 = rkn;
+    int o1k = 0, o1ksh = 0, o1s = 0, o1ssh = 0, o1v = 0, o1vsh = 0;
+    if constexpr (SPL) {
+        int A1k = 0, A1s = 0, A1v = 0;
+        rk1 = rs_row(og.kc1, og.r1k, &A1k);
+        rv1 = rs_row(og.vc1, og.r1v, &A1v);
+        rkn1 = rsrc(og.kn1 + row0, ntok * 2);
+        rvn1 = rsrc(og.vn1 + row0, ntok * 2);
+        if constexpr (QJL) {
+            rs1 = rs_row(og.ks1, og.r1s, &A1s);
+            rkr1 = rsrc(og.kr1 + row0, ntok * 2);
+        }
+        const int k1 = A1k + n * og.r1k, s1 = A1s + n * og.r1s, v1 = A1v + n * og.r1v;
+        o1k = k1 & ~3, o1ksh = 8 * (k1 & 3);
+        o1s = s1 & ~3, o1ssh = 8 * (s1 & 3);
+        o1v = v1 & ~3, o1vsh = 8 * (v1 & 3);
+    }
 
     // Per-block data of a wave, in the part the score stage reads (key codes, sign bits and
     // the three norms of token n) and the part the value stage reads (value codes of tokens
     // 4 r + g).
+    // Rows at any byte alignment (SPL) carry one dword more, realigned when processed.
     struct Kd {
-        uint32_t kw[KB];      // key codes of token n, dims [32 g, 32 g + 32)
-        uint32_t sw;          // sign bits of token n, same dims
-        uint32_t kn, kr, vn;  // norms (f16 bits) of token n
+        uint32_t kw[SPL ? KB + 1 : KB];  // key codes of token n, dims [32 g, 32 g + 32)
+        uint32_t sw[SPL ? 2 : 1];        // sign bits of token n, same dims
+        uint32_t kn, kr, vn;             // norms (f16 bits) of token n
     };
     struct Vd {
-        uint32_t vw[4];       // value codes of tokens 4 r + g, the dword holding lane n's chunk start
+        uint32_t vw[SPL ? 8 : 4];  // value codes of tokens 4 r + g, the dword holding lane n's chunk start
+    };
+    // group 1 of a two-group layer: token n's key code, sign and value code rows (from the
+    // dwords holding their first bytes) and norms
+    struct Od {
+        uint32_t k[3], s, v[3];
+        uint32_t kn, kr, vn;
+    };
+    struct OdNone {};
+    using OdT = std::conditional_t<SPL, Od, OdNone>;
+    auto load_o = [&](OdT& O, int rel_) {
+        if constexpr (SPL) {
+            const int rel = __builtin_amdgcn_readfirstlane(rel_);
+            const u32x3 k = __builtin_amdgcn_raw_buffer_load_b96(rk1, o1k, rel * og.r1k, KV_NT);
+            O.k[0] = k.x, O.k[1] = k.y, O.k[2] = k.z;
+            O.s = QJL ? __builtin_amdgcn_raw_buffer_load_b32(rs1, o1s, rel * og.r1s, KV_NT) : 0u;
+            const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rv1, o1v, rel * og.r1v, KV_NT);
+            O.v[0] = v.x, O.v[1] = v.y, O.v[2] = v.z;
+            O.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn1, no, rel * 2, KV_NT);
+            O.kr = QJL ? __builtin_amdgcn_raw_buffer_load_b16(rkr1, no, rel * 2, KV_NT) : 0u;
+            O.vn = __builtin_amdgcn_raw_buffer_load_b16(rvn1, no, rel * 2, KV_NT);
+        }
     };
     auto load_k = [&](Kd& B, int rel_) {
         const int rel = __builtin_amdgcn_readfirstlane(rel_);  // scalar block offset
-        if constexpr (KB == 1) {
+        if constexpr (SPL) {
+            // KB + 1 dwords from the one holding the lane's first byte
+            if constexpr (KB == 1) {
+                const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rk, ko, rel * krow, KV_NT);
+                B.kw[0] = x.x, B.kw[1] = x.y;
+            } else if constexpr (KB == 2) {
+                const u32x3 x = __builtin_amdgcn_raw_buffer_load_b96(rk, ko, rel * krow, KV_NT);
+                B.kw[0] = x.x, B.kw[1] = x.y, B.kw[2] = x.z;
+            } else {
+                const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ko, rel * krow, KV_NT);
+                B.kw[0] = x.x, B.kw[1] = x.y, B.kw[2] = x.z, B.kw[3] = x.w;
+                if constexpr (KB == 4) B.kw[4] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko + 16, rel * krow, KV_NT);
+            }
+        } else if constexpr (KB == 1) {
             B.kw[0] = __builtin_amdgcn_raw_buffer_load_b32(rk, ko, rel * KROW, KV_NT);
         } else if constexpr (KB == 2) {
             const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rk, ko, rel * KROW, KV_NT);
@@ -757,10 +875,16 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             B.kw[0] = w.x, B.kw[1] = w.y, B.kw[2] = w.z, B.kw[3] = w.w;
         }
         if constexpr (QJL) {
-            B.sw = __builtin_amdgcn_raw_buffer_load_b32(rs, so, rel * (D / 8), KV_NT);
+            if constexpr (SPL) {
+                const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, so, rel * srow, KV_NT);
+                B.sw[0] = x.x, B.sw[1] = x.y;
+            } else {
+                B.sw[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, rel * (D / 8), KV_NT);
+            }
             B.kr = __builtin_amdgcn_raw_buffer_load_b16(rkr, no, rel * 2, KV_NT);
         } else {
-            B.sw = 0u;
+#pragma unroll
+            for (int i = 0; i < (SPL ? 2 : 1); ++i) B.sw[i] = 0u;
             B.kr = 0u;
         }
         B.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn, no, rel * 2, KV_NT);
@@ -770,7 +894,12 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         const int rel = __builtin_amdgcn_readfirstlane(rel_);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            B.vw[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + 4 * r * VROW, rel * VROW, KV_NT);
+            if constexpr (SPL) {
+                const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + 4 * r * vrow, rel * vrow, KV_NT);
+                B.vw[2 * r] = x.x, B.vw[2 * r + 1] = x.y;
+            } else {
+                B.vw[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo + 4 * r * VROW, rel * VROW, KV_NT);
+            }
         }
     };
 
@@ -785,11 +914,12 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // i's first wait would also wait for block i + 1.  For the same reason the load order is
     // pinned with scheduling barriers here as in the loop: the waits at the loop head hold for
     // both ways in, and first loads issued in another order would force a wait for all of them.
-    constexpr int NSET = Cfg<VB, GC, QJL>::NSET;
-    constexpr int NB = Cfg<VB, GC, QJL>::NB;
+    constexpr int NSET = Cfg<VB, GC, QJL, SPL>::NSET;
+    constexpr int NB = Cfg<VB, GC, QJL, SPL>::NB;
     static_assert(NSET % NB == 0, "register sets come in whole steps");
     Kd kset[NSET];
     Vd vset[NSET];
+    OdT oset[NSET];
 
     // ------------------------------------------------------------ prologue
     // phase 1: codebooks and the group's q-side products (every split workgroup of the group
@@ -801,6 +931,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // (PRO_SETS register sets before the products, the rest after them), whose HBM latency the
     // rest of the prologue covers
     float ck_e, cv_e;
+    float c1k_e = 0.0f, c1v_e = 0.0f;  // group 1's codebooks (two-group layers), entry tid
     // int8 keys: the key codebook in fixed point, |Ck| 2^E < 2^15 (wave-uniform scalar loads)
     int E = 0;
     if constexpr (KI8) {
@@ -811,19 +942,23 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         if (cmax > 0.0f) (void)frexpf(cmax, &e);  // cmax < 2^e
         E = 15 - e;
     }
-    constexpr int PRO_SETS = Cfg<VB, GC, QJL>::PRO_SETS;
+    constexpr int PRO_SETS = Cfg<VB, GC, QJL, SPL>::PRO_SETS;
     image_products<QJL, GC, NW, KI8>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, sm.u.pro.qst[wave], wave, lane, [&] {
         ck_e = Ck[tid & ((1 << KB) - 1)];
         cv_e = Cv[tid & ((1 << VB) - 1)];
+        if constexpr (SPL) {
+            if (tid < (1 << og.b1k)) c1k_e = og.Ck1[tid];
+            if (tid < (1 << og.b1v)) c1v_e = og.Cv1[tid];
+        }
 #pragma unroll
         for (int s = 0; s < PRO_SETS; ++s) {
-            load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
+            load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP), load_o(oset[s], first + s * STEP);
             __builtin_amdgcn_sched_barrier(0);
         }
     });
 #pragma unroll
     for (int s = PRO_SETS; s < NSET; ++s) {
-        load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
+        load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP), load_o(oset[s], first + s * STEP);
         __builtin_amdgcn_sched_barrier(0);
     }
     // pair tables from the codebook entries in the lanes (lane l holds Ck[l mod 2^KB] and
@@ -871,11 +1006,24 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // the weight transpose starts zeroed: the loop writes only the halves and rows that hold
     // weights, the rest of the value MFMAs' A operand stays zero
     for (int i = tid; i < (int)(sizeof(sm.wt) / 4); i += NT) (&sm.wt[0][0][0][0])[i] = 0u;
+    if constexpr (SPL) {
+        if (tid < 256) sm.ol.ck[tid] = c1k_e, sm.ol.cv[tid] = c1v_e;
+    }
     __syncthreads();
-    // phase 2 (LDS only): the QJL limb image and the int8 key image
+    // phase 2 (LDS only): the QJL limb image and the int8 key image (group 0's dims only), and
+    // group 1's q-side values of a two-group layer
+    const int d0 = SPL ? og.d0 : D;
     int G2 = 0, F = 0;
-    if constexpr (QJL) G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid);
-    if constexpr (KI8) F = key_image_i8<NT>(sm.u.pro.ps, img, tid);
+    if constexpr (QJL) G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid, d0);
+    if constexpr (KI8) F = key_image_i8<NT>(sm.u.pro.ps, img, tid, d0);
+    if constexpr (SPL) {
+        if (tid < 4 * 2 * OD1) {
+            const int h = tid / (2 * OD1), w = (tid / OD1) & 1, j = tid % OD1;
+            float x = 0.0f;
+            if (j < og.d1) x = w ? sm.u.pro.ps.qp[h][d0 + j] * og.cq1 : sm.u.pro.ps.qr[h][d0 + j];
+            sm.ol.q1[h][w][j] = x;
+        }
+    }
     if constexpr (QJL || KI8) __syncthreads();
     // phase 3: operands into registers.  A operands of the key-score MFMAs: int8 keys, lane
     // (row 4 h + s, g), MFMA j: digits of dims 32 g + 8 j .. + 7 (16 VGPRs); bf16 keys, lane
@@ -886,6 +1034,20 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
     // scores come out of the key MFMAs in units of kscale (int8: 2^-(F + E)) and are taken to
     // log2 units by an fma that is already there; the QJL term is scaled to the same units
     const float kscale = KI8 ? ldexpf(1.0f, -(F + E)) : 1.0f;
+    // group 1 of a two-group layer, for lane group g's head: q_rot (log2 units) and q_proj
+    // (times group 1's QJL scale) of dims d0 .. d0 + OD - 1, zero past d1, so the codes read
+    // there add nothing; the group's value sums o1, rescaled with the MFMA sums
+    float q1r[SPL ? OD : 1], q1p[SPL ? OD : 1], o1[SPL ? OD : 1], sq1 = 0.0f;
+    const float ikscale = 1.0f / kscale;  // a power of two
+    if constexpr (SPL) {
+#pragma unroll
+        for (int j = 0; j < OD; ++j) {
+            q1r[j] = sm.ol.q1[g][0][j];
+            q1p[j] = sm.ol.q1[g][1][j];
+            sq1 += q1p[j];
+            o1[j] = 0.0f;
+        }
+    }
     // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
     // 32 g + 4 jj + v + 8 e.
     u32x4 qj[R::NQJ][2];
@@ -978,6 +1140,21 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         i32x4 acc_i[NB];
         f32x4 acc_k[NB], acc_k1[NB];
         i32x4 acc_q[NB][R::NQJ];
+        // key code and sign words of token n (rows at any byte alignment realigned)
+        uint32_t kwa[NB][KB], swa[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const Kd& B = kset[s0 + b];
+            if constexpr (SPL) {
+#pragma unroll
+                for (int i = 0; i < KB; ++i) kwa[b][i] = __builtin_amdgcn_alignbit(B.kw[i + 1], B.kw[i], kalign);
+                swa[b] = __builtin_amdgcn_alignbit(B.sw[1], B.sw[0], salign);
+            } else {
+#pragma unroll
+                for (int i = 0; i < KB; ++i) kwa[b][i] = B.kw[i];
+                swa[b] = B.sw[0];
+            }
+        }
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -993,28 +1170,26 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             if constexpr (Sm::KWIN) {
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
-                    const Kd& B = kset[s0 + b];
-                    ksh[b][0] = __builtin_amdgcn_alignbit(B.kw[1], B.kw[0], 4);
-                    ksh[b][1] = __builtin_amdgcn_alignbit(B.kw[2], B.kw[1], 4);
-                    ksh[b][2] = B.kw[2] >> 4;
+                    ksh[b][0] = __builtin_amdgcn_alignbit(kwa[b][1], kwa[b][0], 4);
+                    ksh[b][1] = __builtin_amdgcn_alignbit(kwa[b][2], kwa[b][1], 4);
+                    ksh[b][2] = kwa[b][2] >> 4;
                 }
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
-                    const Kd& B = kset[s0 + b];
                     u32x4 bk;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         uint32_t off;
                         if constexpr (KB == 4) {
                             // code byte i of dword j: LDS byte offset 256 * byte + kplane in one v_perm
-                            off = __builtin_amdgcn_perm(B.kw[j], kplane, 0x0C0C0000u | ((4u + (uint32_t)i) << 8));
+                            off = __builtin_amdgcn_perm(kwa[b][j], kplane, 0x0C0C0000u | ((4u + (uint32_t)i) << 8));
                         } else if constexpr (Sm::KWIN) {
-                            off = win_off(B.kw, ksh[b], KB * (8 * j + 2 * i), kwin);
+                            off = win_off(kwa[b], ksh[b], KB * (8 * j + 2 * i), kwin);
                         } else {
-                            off = field_x<2 * KB, 8>(B.kw, KB * (8 * j + 2 * i)) | kplane;
+                            off = field_x<2 * KB, 8>(kwa[b], KB * (8 * j + 2 * i)) | kplane;
                         }
                         bk[i] = *reinterpret_cast<const uint32_t*>(tb0 + off);
                     }
@@ -1027,11 +1202,10 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             for (int j = 0; j < 8; ++j) {
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
-                    const Kd& B = kset[s0 + b];
                     u32x4 bk;
 #pragma unroll
                     for (int p = 0; p < 2; ++p) {
-                        const uint32_t off = field_x<2 * KB, KSHIFT>(B.kw, (4 * j + 2 * p) * KB) | kplane;
+                        const uint32_t off = field_x<2 * KB, KSHIFT>(kwa[b], (4 * j + 2 * p) * KB) | kplane;
                         const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(sm.ktab) + off);
                         bk[2 * p] = e.x;
                         bk[2 * p + 1] = e.y;
@@ -1050,7 +1224,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) bq[jj][v] = kset[s0 + b].sw & (0x01010101u << (4 * jj + v));
+                    for (int v = 0; v < 4; ++v) bq[jj][v] = swa[b] & (0x01010101u << (4 * jj + v));
 #pragma unroll
                 for (int set = 0; set < R::NQJ; ++set) {
                     acc_q[b][set] = mfma_i8(qj[set][0], bq[0], i32x4{0, 0, 0, 0});
@@ -1059,6 +1233,28 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             }
         }
         __builtin_amdgcn_s_setprio(0);
+        // ---- group 1's score terms of a two-group layer (log2 units), token n, head g:
+        // |k1| sum_j q_rot[j] Ck1[code_j] + |r1| (2 sum_{s_j = 1} q_proj[j] - sum_j q_proj[j])
+        float l1[NB];
+        if constexpr (SPL) {
+            const uint64_t m1k = (1ull << og.b1k) - 1u;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const Od& O = oset[s0 + b];
+                const uint64_t kb = ((uint64_t)__builtin_amdgcn_alignbit(O.k[2], O.k[1], o1ksh) << 32) |
+                                    __builtin_amdgcn_alignbit(O.k[1], O.k[0], o1ksh);
+                const uint32_t sb = O.s >> o1ssh;
+                float a = 0.0f, qs = 0.0f;
+#pragma unroll
+                for (int j = 0; j < OD; ++j) {
+                    const uint32_t c = (uint32_t)((kb >> (j * og.b1k)) & m1k);
+                    a = __builtin_fmaf(q1r[j], sm.ol.ck[c], a);
+                    if constexpr (QJL) qs += ((sb >> j) & 1u) ? q1p[j] : 0.0f;
+                }
+                const float v = tq::f16_to_f32(O.kn) * a;
+                l1[b] = QJL ? __builtin_fmaf(tq::f16_to_f32(O.kr), __builtin_fmaf(2.0f, qs, -sq1), v) : v;
+            }
+        }
         // ---- scores
         bool over = false;
 #pragma unroll
@@ -1089,6 +1285,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                 } else {
                     v = knf * ksum;
                 }
+                if constexpr (SPL) v = __builtin_fmaf(l1[b], ikscale, v);
                 lg[b][i] = valid ? v : NEG_INF;
                 over |= __builtin_fmaf(lg[b][i], kscale, ev[b]) > m_thr[i];
             }
@@ -1115,12 +1312,17 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                         }
                     }
                 }
+                if constexpr (SPL) {
+#pragma unroll
+                    for (int j = 0; j < OD; ++j) o1[j] *= a;
+                }
                 m_ref[i] = mn;
                 m_thr[i] = mn + (WEXP0 + LAZY_MAX);
             }
         }
         // ---- weights
         u32x4 av[NB];
+        float pv1[NB];  // group 1: p |v1| of token n (head g)
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             uint32_t(*wt)[WROW] = sm.wt[wave][b];
@@ -1128,6 +1330,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
             for (int i = 0; i < R::HPL; ++i) {
                 const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[b][i], kscale, -m_ref[i]));
+                if constexpr (SPL) pv1[b] = p * tq::f16_to_f32(oset[s0 + b].vn);
                 s_lane[i] += p;
                 const uint16_t w = (uint16_t)tq::f32_to_f16(__builtin_fmaf(vnf, p, 0.0f));
                 const int h = R::HPL * g + i;
@@ -1143,8 +1346,10 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
         for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t w = vset[s0 + b].vw[i];
-                if constexpr (VB == 3)
+                const uint32_t w = vset[s0 + b].vw[SPL ? 2 * i : i];
+                if constexpr (SPL)
+                    ch[b][i] = __builtin_amdgcn_alignbit(vset[s0 + b].vw[2 * i + 1], w, vsh);
+                else if constexpr (VB == 3)
                     ch[b][i] = chunk3(w, vsh);
                 else if constexpr (VB < 3)
                     ch[b][i] = w >> vsh;
@@ -1176,6 +1381,19 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
             }
         }
         __builtin_amdgcn_s_setprio(0);
+        // ---- group 1's value sums of a two-group layer: o1[j] += p |v1| Cv1[code_j]
+        if constexpr (SPL) {
+            const uint64_t m1v = (1ull << og.b1v) - 1u;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const Od& O = oset[s0 + b];
+                const uint64_t vb = ((uint64_t)__builtin_amdgcn_alignbit(O.v[2], O.v[1], o1vsh) << 32) |
+                                    __builtin_amdgcn_alignbit(O.v[1], O.v[0], o1vsh);
+#pragma unroll
+                for (int j = 0; j < OD; ++j)
+                    o1[j] = __builtin_fmaf(pv1[b], sm.ol.cv[(uint32_t)((vb >> (j * og.b1v)) & m1v)], o1[j]);
+            }
+        }
     };
 
     // (the first NSET blocks were issued in the prologue)
@@ -1193,7 +1411,8 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int b = 0; b < NB; ++b)
-                    load_k(kset[s + b], rel + (NSET + b) * STEP), load_v(vset[s + b], rel + (NSET + b) * STEP);
+                    load_k(kset[s + b], rel + (NSET + b) * STEP), load_v(vset[s + b], rel + (NSET + b) * STEP),
+                        load_o(oset[s + b], rel + (NSET + b) * STEP);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -1218,6 +1437,15 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL>::NT)) void split_kernel(
 #pragma unroll
                 for (int b = 1; b < NB; ++b) o += acc_v[b][u][r];
                 sm.u.epi.o[wave][h][8 * n + 2 * u + p] = o;
+            }
+        }
+        if constexpr (SPL) {
+            // group 1's dims d0 .. D - 1 replace the MFMA sums there (which summed the codes
+            // read past group 0's rows); the wave's LDS writes execute in program order
+#pragma unroll
+            for (int j = 0; j < OD; ++j) {
+                const float t = row_sum16(o1[j]);
+                if (n == 0 && j < og.d1) sm.u.epi.o[wave][h][og.d0 + j] = t;
             }
         }
         if (n == 0) {
@@ -1268,6 +1496,7 @@ struct SplitArgs {
     int64_t tps;
     int n_split;
     float *po, *pml;
+    Og og;  // two-group layers only
 };
 
 int cu_count() {
@@ -1280,13 +1509,13 @@ int cu_count() {
     });
 }
 
-template <int KB, int VB, bool QJL, int GC>
+template <int KB, int VB, bool QJL, int GC, int OD = 0>
 int wgs_per_cu() {
     static std::atomic<int64_t> cached[tq::MAX_DEVICES];
     return (int)tq::once_per_device(cached, 1, [](int) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC>, Cfg<VB, GC, QJL>::NT, 0) !=
-                hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC, OD>,
+                                                         Cfg<VB, GC, QJL, (OD > 0)>::NT, 0) != hipSuccess ||
             o < 1)
             o = 1;
         return (int64_t)o;
@@ -1309,21 +1538,46 @@ int choose_split(int groups, int64_t n_tokens, int target_wgs, int nw, int64_t* 
     return (int)(got > 0 ? got : 1);
 }
 
-template <int KB, int VB, bool QJL, int GC>
+template <int KB, int VB, bool QJL, int GC, int OD = 0>
 int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out, int64_t* tps_out) {
-    const int target = wgs_per_cu<KB, VB, QJL, GC>() * cu_count();
+    constexpr bool SPL = OD > 0;
+    const int target = wgs_per_cu<KB, VB, QJL, GC, OD>() * cu_count();
     int64_t tps;
-    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC, QJL>::NW, &tps);
+    const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC, QJL, SPL>::NW, &tps);
     *n_split_out = ns;
     *tps_out = tps;
     // a workgroup's range stays below 2^24 tokens: its byte ranges fit the 31-bit buffer
     // descriptors and its token offsets fit 32-bit scalars
     if (tps >= ((int64_t)1 << 24)) return TQ_ERR_UNSUPPORTED;
     if (a.po == nullptr) return TQ_OK;  // sizing query only
-    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC>), dim3(ns, groups), dim3(Cfg<VB, GC, QJL>::NT), 0, s, a.q, a.q_heads,
-                       a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks, a.kr, a.vc,
-                       a.vn, a.Rk, a.S, a.c_mse, a.c_qjl, a.Ck, a.Cv, a.scale, tps, ns, a.po, a.pml);
+    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC, OD>), dim3(ns, groups), dim3(Cfg<VB, GC, QJL, SPL>::NT), 0, s,
+                       a.q, a.q_heads, a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks,
+                       a.kr, a.vc, a.vn, a.Rk, a.S, a.c_mse, a.c_qjl, a.Ck, a.Cv, a.scale, tps, ns, a.po, a.pml, a.og);
     return TQ_OK;
+}
+
+// Two-group layers on the split kernel (at most 4 heads per KV head; group 1 at most OD1
+// channels): group 0's bit widths as for a one-group layer, OD = 4 or 8 per-lane dims.
+template <int KB, int VB, bool QJL>
+int launch_split_og(const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
+    if (a.og.d1 <= 4) return launch_split<KB, VB, QJL, 1, 4>(a, groups, s, ns, tps);
+    return launch_split<KB, VB, QJL, 1, OD1>(a, groups, s, ns, tps);
+}
+
+int dispatch_og(int value_bits, int has_qjl, const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
+    if (has_qjl) {
+        switch (value_bits) {
+            case 2: return launch_split_og<1, 2, true>(a, groups, s, ns, tps);
+            case 3: return launch_split_og<2, 3, true>(a, groups, s, ns, tps);
+            default: return launch_split_og<3, 4, true>(a, groups, s, ns, tps);
+        }
+    }
+    switch (value_bits) {
+        case 1: return launch_split_og<1, 1, false>(a, groups, s, ns, tps);
+        case 2: return launch_split_og<2, 2, false>(a, groups, s, ns, tps);
+        case 3: return launch_split_og<3, 3, false>(a, groups, s, ns, tps);
+        default: return launch_split_og<4, 4, false>(a, groups, s, ns, tps);
+    }
 }
 
 template <int KB, int VB, bool QJL>
@@ -1870,6 +2124,50 @@ extern "C" int tq_decode_attention_groups(const uint16_t* q, int batch, int q_he
     }
     if (dsum != D) return TQ_ERR_INVALID_ARGUMENT;  // the groups partition the head's channels
     const int groups = batch * kv_heads;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // Two groups with at most 4 query heads per KV head and at most OD1 outlier channels: the
+    // split kernel's matrix-core stages for group 0 and a per-lane term for group 1, when group
+    // 0's bit widths are a one-group layer's and the row arrays start at 4-byte boundaries
+    const auto a4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; };
+    const bool og_bits = has_qjl ? (key_bits[0] + 1 == value_bits[0] && value_bits[0] >= 2 && value_bits[0] <= 4)
+                                 : (key_bits[0] == value_bits[0] && key_bits[0] >= 1 && key_bits[0] <= 4);
+    bool og_ok = n_groups == 2 && G <= 4 && sub_dims[1] <= OD1 && og_bits && aligned16(q);
+    for (int g = 0; og_ok && g < 2; ++g)
+        og_ok = a4(k_codes[g]) && a4(v_codes[g]) && (!has_qjl || a4(k_signs[g]));
+    if (og_ok) {
+        const int d0 = sub_dims[0], d1 = sub_dims[1];
+        const double qs = sqrt(M_PI / 2.0);
+        SplitArgs sa{q,        q_heads,   kv_heads,  G,          seq_starts,
+                     seq_lens, n_tokens,  cap,       k_codes[0], k_norms[0],
+                     has_qjl ? k_signs[0] : nullptr, has_qjl ? k_rnorms[0] : nullptr, v_codes[0], v_norms[0],
+                     key_matrix, qjl_matrix, scale * LOG2E, (float)(scale * LOG2E * (qs / d0)), key_centers[0],
+                     value_centers[0], scale, 0, 0, nullptr, nullptr};
+        Og& o = sa.og;
+        o.d0 = d0, o.d1 = d1;
+        o.r0k = a.rk[0], o.r0s = a.rs[0], o.r0v = a.rv[0];
+        o.r1k = a.rk[1], o.r1s = a.rs[1], o.r1v = a.rv[1];
+        o.b1k = key_bits[1], o.b1v = value_bits[1];
+        o.kc1 = k_codes[1], o.ks1 = has_qjl ? k_signs[1] : nullptr, o.vc1 = v_codes[1];
+        o.kn1 = k_norms[1], o.kr1 = has_qjl ? k_rnorms[1] : nullptr, o.vn1 = v_norms[1];
+        o.Ck1 = key_centers[1], o.Cv1 = value_centers[1];
+        o.cq1 = (float)(scale * LOG2E * (qs / d1));
+        int n_split = 0;
+        int64_t tps = 0;
+        int st = dispatch_og(value_bits[0], has_qjl, sa, groups, s, &n_split, &tps);  // sizing
+        if (st != TQ_OK) return st;
+        const Ws w = ws_layout(batch, q_heads, n_split);
+        if (workspace_bytes < w.total) return TQ_ERR_WORKSPACE;
+        char* base = static_cast<char*>(workspace);
+        sa.po = reinterpret_cast<float*>(base + w.po);
+        sa.pml = reinterpret_cast<float*>(base + w.pml);
+        st = dispatch_og(value_bits[0], has_qjl, sa, groups, s, &n_split, &tps);
+        if (st != TQ_OK) return st;
+        TQ_CHECK_LAUNCH();
+        hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(MT), 0, s, sa.po, sa.pml, n_split, value_matrix,
+                           out_f32, out_bf16, lse_out);
+        TQ_CHECK_LAUNCH();
+        return TQ_OK;
+    }
     int64_t tps = 0;
     const int n_split = group_split(groups, n_tokens > 0 ? n_tokens : 1, &tps);
     const Ws w = ws_layout(batch, q_heads, n_split);
@@ -1880,7 +2178,6 @@ extern "C" int tq_decode_attention_groups(const uint16_t* q, int batch, int q_he
     a.tps = tps;
     a.n_split = n_split;
     const size_t lds = (size_t)(kst > vst ? kst : vst) * sizeof(uint32_t);
-    hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(n_split, groups);
     if (G <= 4) {
         if (has_qjl) hipLaunchKernelGGL((group_attn_kernel<4, true>), grid, dim3(GT), lds, s, a);

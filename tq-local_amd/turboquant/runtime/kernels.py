@@ -91,7 +91,8 @@ class GroupCodec:
     ``rotation`` / ``qjl`` are the group's own d x d matrices (the reference's
     attributes); ``rotation_ch`` / ``qjl_ch`` are the same matrices in channel
     space (``group_matrix``), which is what libtq takes.  ``qjl`` is set only for
-    Q_prod key groups.
+    Q_prod key groups.  ``attn_centers`` caches a value group's fp16 codebook for the
+    decode attention (``attention_value_centers``).
     """
 
     channels: np.ndarray  # int32 [d], host, strictly ascending
@@ -102,6 +103,7 @@ class GroupCodec:
     rotation_ch: torch.Tensor  # fp32 [D, D]
     qjl: torch.Tensor | None = None  # fp32 [d, d]
     qjl_ch: torch.Tensor | None = None  # fp32 [D, D]
+    attn_centers: torch.Tensor | None = None  # fp32 [2^bits], fp16-exact values
 
     @property
     def dim(self) -> int:
@@ -290,11 +292,13 @@ def value_codebook_f16(centers: np.ndarray, bits: int, dim: int = HEAD_DIM) -> n
     return out
 
 
-def attention_value_centers(codec: CodecParams) -> torch.Tensor:
+def attention_value_centers(codec: CodecParams | GroupCodec) -> torch.Tensor:
     """The value codebook tq_decode_attention is given: ``value_codebook_f16`` of the
-    codec's centers, on the codec's device, computed once per codec."""
+    codec's centers (at the group's dimension for a channel group), on the codec's
+    device, computed once per codec."""
     if codec.attn_centers is None:
-        host = value_codebook_f16(codec.centers.detach().cpu().numpy(), codec.bits)
+        dim = codec.dim if isinstance(codec, GroupCodec) else HEAD_DIM
+        host = value_codebook_f16(codec.centers.detach().cpu().numpy(), codec.bits, dim)
         codec.attn_centers = torch.from_numpy(host).to(codec.centers.device)
     return codec.attn_centers
 
@@ -398,7 +402,12 @@ def decode_attention_groups(q: torch.Tensor, groups: list[dict], *, n_tokens: in
     ks = ptr("k_signs") if has_qjl else None
     kr = ptr("k_rnorms") if has_qjl else None
     ck = arr(P, [g["key"].centers.data_ptr() for g in groups])
-    cv = arr(P, [g["value"].centers.data_ptr() for g in groups])
+    # with two groups the normal group's value sums may run in fp16 on the matrix cores: its
+    # codebook goes in the fp16 form that keeps long-context sums unbiased
+    vcen = [g["value"].centers for g in groups]
+    if n == 2 and groups[0]["value"].bits <= 4:
+        vcen[0] = attention_value_centers(groups[0]["value"])
+    cv = arr(P, [c.data_ptr() for c in vcen])
     keep += [dims, kbits, vbits, kc, kn, vc, vn, ks, kr, ck, cv]
     out_bf16 = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=q.device)
     out_f32 = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device) if want_f32 else None
