@@ -264,20 +264,27 @@ struct PrepLds {
     float red[16];                    // max |.| per matrix-core tile: R_k tiles 0..7, S tiles 8..15
 };
 
-// The outlier group of a two-group layer (SPL): at most OD1 channels, handled per lane in fp32
+// The outlier group of a two-group layer: OD (4 or 8) dims per lane, in fp32.  Code pairs are
+// looked up in pair tables of (C[c0], C[c1]) where the widths allow (keys up to 4 bits, values
+// up to 5 bits with OD = 4, 4 with OD = 8), single codes in the codebooks otherwise.
 constexpr int OD1 = 8;
-template <bool SPL>
+template <int OD>
 struct OutLds {
-    float q1[4][2][OD1];  // per query head: q_rot (log2 units) and q_proj (times the QJL scale) of the group's dims
-    float ck[256];        // the group's key and value codebooks (up to 8 bits)
+    static constexpr int KP = 256, VP = OD == 4 ? 1024 : 256;  // pair-table entries
+    float q1[4][OD];        // per query head: q_rot of the group's dims (log2 units)
+    float ts[4][1 << OD];   // per query head: sum of q_proj (times the QJL scale) over the dims whose sign bit is set
+    float ck[256];          // the group's key and value codebooks (up to 8 bits)
     float cv[256];
+    float2 tk[KP];          // key code pairs
+    float2 tv[VP];          // value code pairs
 };
 template <>
-struct OutLds<false> {};
+struct OutLds<0> {};
 
-template <int KB, int VB, bool QJL, int GC, bool SPL = false>
+template <int KB, int VB, bool QJL, int GC, int OD = 0>
 struct Smem {
     static constexpr int NH = 4 * GC;
+    static constexpr bool SPL = OD > 0;
     static constexpr int NW = Cfg<VB, GC, QJL, SPL>::NW;
     static constexpr bool KI8 = GC == 1;
     // Byte windows (3-bit codes): the 6-bit field of a code pair is looked up by a byte of the
@@ -307,7 +314,7 @@ struct Smem {
         } epi;
     } u;
     uint32_t wt[NW][Cfg<VB, GC, QJL, SPL>::NB][16][WROW];   // per-wave transposes of the softmax weights
-    OutLds<SPL> ol;
+    OutLds<OD> ol;
 };
 
 // LDS byte offset (from T0's base) of the table entry of the 6-bit field at bit p of the word
@@ -689,7 +696,9 @@ struct Og {
     float cq1;          // the logit scale (log2 units) times sqrt(pi/2) / d1
 };
 
-template <int KB, int VB, bool QJL, int GC, int OD = 0>
+// X1 > 0: group 1's widths are group 0's plus X1 (the reference's default outlier_extra_bits
+// is 1), compile-time constants; X1 = 0: the widths come from og at run time.
+template <int KB, int VB, bool QJL, int GC, int OD = 0, int X1 = 0>
 __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel(
     const uint16_t* __restrict__ q, int q_heads, int kv_heads, int G, const int32_t* __restrict__ seq_starts,
     const int32_t* __restrict__ seq_lens, int64_t n_tokens, int64_t cap, const uint8_t* __restrict__ kc,
@@ -700,7 +709,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml, Og og) {
     constexpr bool SPL = OD > 0;
     static_assert(!SPL || (GC == 1 && OD <= OD1), "two-group layers: at most 4 heads per KV head, OD <= OD1");
-    using Sm = Smem<KB, VB, QJL, GC, SPL>;
+    using Sm = Smem<KB, VB, QJL, GC, OD>;
     using R = Rows<GC>;
     constexpr bool KI8 = Sm::KI8;
     constexpr int NW = Cfg<VB, GC, QJL, SPL>::NW;
@@ -797,7 +806,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     // group 1 of a two-group layer: token n's rows (at most 8 bytes each) from the dword
     // holding their first byte, and its three norms
     __amdgpu_buffer_rsrc_t rk1 = rkn, rs1 = rkn, rv1 = rkn, rkn1 = rkn, rkr1 = rkn, rvn1 = rkn;
-    int o1k = 0, o1ksh = 0, o1s = 0, o1ssh = 0, o1v = 0, o1vsh = 0;
+    int o1k = 0, o1ksh = 0, o1s = 0, o1ssh = 0, o1v = 0, o1vsh = 0, o1n = 0;
     if constexpr (SPL) {
         int A1k = 0, A1s = 0, A1v = 0;
         rk1 = rs_row(og.kc1, og.r1k, &A1k);
@@ -809,9 +818,13 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
             rkr1 = rsrc(og.kr1 + row0, ntok * 2);
         }
         const int k1 = A1k + n * og.r1k, s1 = A1s + n * og.r1s, v1 = A1v + n * og.r1v;
-        o1k = k1 & ~3, o1ksh = 8 * (k1 & 3);
-        o1s = s1 & ~3, o1ssh = 8 * (s1 & 3);
-        o1v = v1 & ~3, o1vsh = 8 * (v1 & 3);
+        // lanes 32..63 read the round's second block, STEP tokens on (a multiple of 16 rows,
+        // so the same byte shifts)
+        const int hb = g >= 2 ? NW * BLK : 0;
+        o1k = (k1 & ~3) + hb * og.r1k, o1ksh = 8 * (k1 & 3);
+        o1s = (s1 & ~3) + hb * og.r1s, o1ssh = 8 * (s1 & 3);
+        o1v = (v1 & ~3) + hb * og.r1v, o1vsh = 8 * (v1 & 3);
+        o1n = no + 2 * hb;
     }
 
     // Per-block data of a wave, in the part the score stage reads (key codes, sign bits and
@@ -826,8 +839,11 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     struct Vd {
         uint32_t vw[SPL ? 8 : 4];  // value codes of tokens 4 r + g, the dword holding lane n's chunk start
     };
-    // group 1 of a two-group layer: token n's key code, sign and value code rows (from the
-    // dwords holding their first bytes) and norms
+    // group 1 of a two-group layer, for the two blocks of a round (NSET = 2 blocks STEP tokens
+    // apart; lanes 0..31 hold the first, lanes 32..63 the second, each block's half reaching all
+    // lanes through v_permlane32_swap): token n's key code, sign and value code rows (from the
+    // dwords holding their first bytes) and norms.  One load instruction per array serves two
+    // blocks (six per block measured ~18 us per call slower at the C2 split shape).
     struct Od {
         uint32_t k[3], s, v[3];
         uint32_t kn, kr, vn;
@@ -842,9 +858,9 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
             O.s = QJL ? __builtin_amdgcn_raw_buffer_load_b32(rs1, o1s, rel * og.r1s, KV_NT) : 0u;
             const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rv1, o1v, rel * og.r1v, KV_NT);
             O.v[0] = v.x, O.v[1] = v.y, O.v[2] = v.z;
-            O.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn1, no, rel * 2, KV_NT);
-            O.kr = QJL ? __builtin_amdgcn_raw_buffer_load_b16(rkr1, no, rel * 2, KV_NT) : 0u;
-            O.vn = __builtin_amdgcn_raw_buffer_load_b16(rvn1, no, rel * 2, KV_NT);
+            O.kn = __builtin_amdgcn_raw_buffer_load_b16(rkn1, o1n, rel * 2, KV_NT);
+            O.kr = QJL ? __builtin_amdgcn_raw_buffer_load_b16(rkr1, o1n, rel * 2, KV_NT) : 0u;
+            O.vn = __builtin_amdgcn_raw_buffer_load_b16(rvn1, o1n, rel * 2, KV_NT);
         }
     };
     auto load_k = [&](Kd& B, int rel_) {
@@ -919,7 +935,8 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     static_assert(NSET % NB == 0, "register sets come in whole steps");
     Kd kset[NSET];
     Vd vset[NSET];
-    OdT oset[NSET];
+    static_assert(!SPL || (NSET == 2 && NB == 1), "two-group layers: group 1's loads serve the two blocks of a round");
+    OdT oset[2];  // two-group layers: rounds of even / odd parity
 
     // ------------------------------------------------------------ prologue
     // phase 1: codebooks and the group's q-side products (every split workgroup of the group
@@ -952,15 +969,19 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
         }
 #pragma unroll
         for (int s = 0; s < PRO_SETS; ++s) {
-            load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP), load_o(oset[s], first + s * STEP);
+            load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
+            if (s == 0) load_o(oset[0], first);
             __builtin_amdgcn_sched_barrier(0);
         }
     });
 #pragma unroll
     for (int s = PRO_SETS; s < NSET; ++s) {
-        load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP), load_o(oset[s], first + s * STEP);
+        load_k(kset[s], first + s * STEP), load_v(vset[s], first + s * STEP);
+        if (s == 0) load_o(oset[0], first);  // rounds 0 and 1 (two blocks each)
         __builtin_amdgcn_sched_barrier(0);
     }
+    load_o(oset[1], first + NSET * STEP);
+    __builtin_amdgcn_sched_barrier(0);
     // pair tables from the codebook entries in the lanes (lane l holds Ck[l mod 2^KB] and
     // Cv[l mod 2^VB]; ds_bpermute), four copies of an entry per 16-byte write, by the older half
     // of the waves: they finish their products first and wait at the barrier below for the
@@ -1016,13 +1037,32 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     int G2 = 0, F = 0;
     if constexpr (QJL) G2 = qjl_image<GC, NT>(sm.u.pro.ps, img, tid, d0);
     if constexpr (KI8) F = key_image_i8<NT>(sm.u.pro.ps, img, tid, d0);
+    // group 1 of a two-group layer: its code widths (constants with X1 > 0) and the widths whose
+    // code pairs have tables
+    const int b1k = X1 > 0 ? KB + X1 : og.b1k, b1v = X1 > 0 ? VB + X1 : og.b1v;
+    const bool kpair = SPL && b1k <= 4, vpair = SPL && b1v <= (OD == 4 ? 5 : 4);
     if constexpr (SPL) {
-        if (tid < 4 * 2 * OD1) {
-            const int h = tid / (2 * OD1), w = (tid / OD1) & 1, j = tid % OD1;
-            float x = 0.0f;
-            if (j < og.d1) x = w ? sm.u.pro.ps.qp[h][d0 + j] * og.cq1 : sm.u.pro.ps.qr[h][d0 + j];
-            sm.ol.q1[h][w][j] = x;
+        // q_rot of group 1's dims per head (zero past d1), the QJL sign-sum table (ts[h][s] =
+        // sum of q_proj times the QJL scale over the dims whose bit is set in s, in ascending
+        // order) and the code-pair tables (pair index = c0 + c1 2^b, as the two codes lie in
+        // the row)
+        if (tid < 4 * OD) {
+            const int h = tid / OD, j = tid % OD;
+            sm.ol.q1[h][j] = j < og.d1 ? sm.u.pro.ps.qr[h][d0 + j] : 0.0f;
         }
+        for (int i = tid; i < (4 << OD); i += NT) {
+            const int h = i >> OD, sg = i & ((1 << OD) - 1);
+            float t = 0.0f;
+            for (int j = 0; j < og.d1; ++j)
+                if ((sg >> j) & 1) t += sm.u.pro.ps.qp[h][d0 + j] * og.cq1;
+            sm.ol.ts[h][sg] = t;
+        }
+        if (kpair)
+            for (int i = tid; i < (1 << (2 * b1k)); i += NT)
+                sm.ol.tk[i] = make_float2(sm.ol.ck[i & ((1 << b1k) - 1)], sm.ol.ck[i >> b1k]);
+        if (vpair)
+            for (int i = tid; i < (1 << (2 * b1v)); i += NT)
+                sm.ol.tv[i] = make_float2(sm.ol.cv[i & ((1 << b1v) - 1)], sm.ol.cv[i >> b1v]);
     }
     if constexpr (QJL || KI8) __syncthreads();
     // phase 3: operands into registers.  A operands of the key-score MFMAs: int8 keys, lane
@@ -1034,19 +1074,18 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     // scores come out of the key MFMAs in units of kscale (int8: 2^-(F + E)) and are taken to
     // log2 units by an fma that is already there; the QJL term is scaled to the same units
     const float kscale = KI8 ? ldexpf(1.0f, -(F + E)) : 1.0f;
-    // group 1 of a two-group layer, for lane group g's head: q_rot (log2 units) and q_proj
-    // (times group 1's QJL scale) of dims d0 .. d0 + OD - 1, zero past d1, so the codes read
-    // there add nothing; the group's value sums o1, rescaled with the MFMA sums
-    float q1r[SPL ? OD : 1], q1p[SPL ? OD : 1], o1[SPL ? OD : 1], sq1 = 0.0f;
+    // group 1 of a two-group layer, for lane group g's head: q_rot (log2 units) of dims d0 ..
+    // d0 + OD - 1, zero past d1, so the codes read there add nothing; the sum of its q_proj
+    // (times the QJL scale); the group's value sums o1, rescaled with the MFMA sums
+    float q1r[SPL ? OD : 1], o1[SPL ? OD : 1], sq1 = 0.0f;
     const float ikscale = 1.0f / kscale;  // a power of two
     if constexpr (SPL) {
 #pragma unroll
         for (int j = 0; j < OD; ++j) {
-            q1r[j] = sm.ol.q1[g][0][j];
-            q1p[j] = sm.ol.q1[g][1][j];
-            sq1 += q1p[j];
+            q1r[j] = sm.ol.q1[g][j];
             o1[j] = 0.0f;
         }
+        sq1 = sm.ol.ts[g][(1 << OD) - 1];
     }
     // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
     // 32 g + 4 jj + v + 8 e.
@@ -1134,7 +1173,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     // The MFMA stages run at raised wave priority: a wave that reaches its matrix work issues
     // ahead of waves in their VALU/LDS phases, so the SIMD's MFMA and VALU work of different
     // waves overlap more.
-    auto process = [&](int s0, int rel0) {
+    auto process = [&](int s0, int rel0, int op) {
         float lg[NB][R::HPL];
         float ev[NB];
         i32x4 acc_i[NB];
@@ -1235,24 +1274,45 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
         __builtin_amdgcn_s_setprio(0);
         // ---- group 1's score terms of a two-group layer (log2 units), token n, head g:
         // |k1| sum_j q_rot[j] Ck1[code_j] + |r1| (2 sum_{s_j = 1} q_proj[j] - sum_j q_proj[j])
+        // group 1's data of token n of this block (NB = 1): the round's block s0 sits in lane
+        // half s0 of oset[op]; rows realigned before the swap (both blocks share the shifts)
+        uint32_t g1k[2] = {0u, 0u}, g1s = 0u, g1v[2] = {0u, 0u}, g1n = 0u, g1vn = 0u;
+        if constexpr (SPL) {
+            const Od& O = oset[op];
+            const auto half = [&](uint32_t v) {
+                const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+                return s0 == 0 ? (uint32_t)r[0] : (uint32_t)r[1];
+            };
+            g1k[0] = half(__builtin_amdgcn_alignbit(O.k[1], O.k[0], o1ksh));
+            g1k[1] = half(__builtin_amdgcn_alignbit(O.k[2], O.k[1], o1ksh));
+            g1s = half(O.s >> o1ssh);
+            g1v[0] = half(__builtin_amdgcn_alignbit(O.v[1], O.v[0], o1vsh));
+            g1v[1] = half(__builtin_amdgcn_alignbit(O.v[2], O.v[1], o1vsh));
+            g1n = half(__builtin_amdgcn_perm(O.kr, O.kn, 0x05040100u));  // |k1| | |r1| << 16
+            g1vn = half(O.vn);
+        }
         float l1[NB];
         if constexpr (SPL) {
-            const uint64_t m1k = (1ull << og.b1k) - 1u;
+            const uint64_t m1k = (1ull << b1k) - 1u;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const Od& O = oset[s0 + b];
-                const uint64_t kb = ((uint64_t)__builtin_amdgcn_alignbit(O.k[2], O.k[1], o1ksh) << 32) |
-                                    __builtin_amdgcn_alignbit(O.k[1], O.k[0], o1ksh);
-                const uint32_t sb = O.s >> o1ssh;
-                float a = 0.0f, qs = 0.0f;
+                const uint64_t kb = ((uint64_t)g1k[1] << 32) | g1k[0];
+                float a = 0.0f;
+                if (kpair) {
+                    const uint64_t mp = (1ull << (2 * b1k)) - 1u;
 #pragma unroll
-                for (int j = 0; j < OD; ++j) {
-                    const uint32_t c = (uint32_t)((kb >> (j * og.b1k)) & m1k);
-                    a = __builtin_fmaf(q1r[j], sm.ol.ck[c], a);
-                    if constexpr (QJL) qs += ((sb >> j) & 1u) ? q1p[j] : 0.0f;
+                    for (int p = 0; p < OD / 2; ++p) {
+                        const float2 e = sm.ol.tk[(uint32_t)((kb >> (2 * p * b1k)) & mp)];
+                        a = __builtin_fmaf(q1r[2 * p], e.x, a);
+                        a = __builtin_fmaf(q1r[2 * p + 1], e.y, a);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < OD; ++j) a = __builtin_fmaf(q1r[j], sm.ol.ck[(uint32_t)((kb >> (j * b1k)) & m1k)], a);
                 }
-                const float v = tq::f16_to_f32(O.kn) * a;
-                l1[b] = QJL ? __builtin_fmaf(tq::f16_to_f32(O.kr), __builtin_fmaf(2.0f, qs, -sq1), v) : v;
+                const float qs = QJL ? sm.ol.ts[g][g1s & ((1u << OD) - 1u)] : 0.0f;
+                const float v = tq::f16_to_f32(g1n & 0xFFFFu) * a;
+                l1[b] = QJL ? __builtin_fmaf(tq::f16_to_f32(g1n >> 16), __builtin_fmaf(2.0f, qs, -sq1), v) : v;
             }
         }
         // ---- scores
@@ -1330,7 +1390,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
 #pragma unroll
             for (int i = 0; i < R::HPL; ++i) {
                 const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[b][i], kscale, -m_ref[i]));
-                if constexpr (SPL) pv1[b] = p * tq::f16_to_f32(oset[s0 + b].vn);
+                if constexpr (SPL) pv1[b] = p * tq::f16_to_f32(g1vn);
                 s_lane[i] += p;
                 const uint16_t w = (uint16_t)tq::f32_to_f16(__builtin_fmaf(vnf, p, 0.0f));
                 const int h = R::HPL * g + i;
@@ -1383,15 +1443,23 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
         __builtin_amdgcn_s_setprio(0);
         // ---- group 1's value sums of a two-group layer: o1[j] += p |v1| Cv1[code_j]
         if constexpr (SPL) {
-            const uint64_t m1v = (1ull << og.b1v) - 1u;
+            const uint64_t m1v = (1ull << b1v) - 1u;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const Od& O = oset[s0 + b];
-                const uint64_t vb = ((uint64_t)__builtin_amdgcn_alignbit(O.v[2], O.v[1], o1vsh) << 32) |
-                                    __builtin_amdgcn_alignbit(O.v[1], O.v[0], o1vsh);
+                const uint64_t vb = ((uint64_t)g1v[1] << 32) | g1v[0];
+                if (vpair) {
+                    const uint64_t mp = (1ull << (2 * b1v)) - 1u;
 #pragma unroll
-                for (int j = 0; j < OD; ++j)
-                    o1[j] = __builtin_fmaf(pv1[b], sm.ol.cv[(uint32_t)((vb >> (j * og.b1v)) & m1v)], o1[j]);
+                    for (int p = 0; p < OD / 2; ++p) {
+                        const float2 e = sm.ol.tv[(uint32_t)((vb >> (2 * p * b1v)) & mp)];
+                        o1[2 * p] = __builtin_fmaf(pv1[b], e.x, o1[2 * p]);
+                        o1[2 * p + 1] = __builtin_fmaf(pv1[b], e.y, o1[2 * p + 1]);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < OD; ++j)
+                        o1[j] = __builtin_fmaf(pv1[b], sm.ol.cv[(uint32_t)((vb >> (j * b1v)) & m1v)], o1[j]);
+                }
             }
         }
     };
@@ -1403,16 +1471,23 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
         // (not the refill loads, which stay unconditional).  Skipping matters where a workgroup's
         // blocks do not divide evenly among its waves (C4: 128 blocks over 12 waves, -0.8 us per
         // call; C5 shape -1.4)
-        for (int i = 0; i < nb; i += NSET) {
+        // Two-group layers: two rounds per iteration, so that each round's group-1 register set
+        // (refilled with the round two ahead once both its blocks are processed) has a fixed index.
+        constexpr int RPI = SPL ? 2 : 1;  // rounds per iteration
+        for (int i = 0; i < nb; i += RPI * NSET) {
 #pragma unroll
-            for (int s = 0; s < NSET; s += NB) {
-                const int rel = first + (i + s) * STEP;
-                if (rel < nt) process(s, rel);
-                __builtin_amdgcn_sched_barrier(0);
+            for (int rp = 0; rp < RPI; ++rp) {
 #pragma unroll
-                for (int b = 0; b < NB; ++b)
-                    load_k(kset[s + b], rel + (NSET + b) * STEP), load_v(vset[s + b], rel + (NSET + b) * STEP),
-                        load_o(oset[s + b], rel + (NSET + b) * STEP);
+                for (int s = 0; s < NSET; s += NB) {
+                    const int rel = first + (i + rp * NSET + s) * STEP;
+                    if (rel < nt) process(s, rel, rp);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        load_k(kset[s + b], rel + (NSET + b) * STEP), load_v(vset[s + b], rel + (NSET + b) * STEP);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                load_o(oset[rp], first + (i + rp * NSET + 2 * NSET) * STEP);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -1509,12 +1584,12 @@ int cu_count() {
     });
 }
 
-template <int KB, int VB, bool QJL, int GC, int OD = 0>
+template <int KB, int VB, bool QJL, int GC, int OD = 0, int X1 = 0>
 int wgs_per_cu() {
     static std::atomic<int64_t> cached[tq::MAX_DEVICES];
     return (int)tq::once_per_device(cached, 1, [](int) {
         int o = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC, OD>,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, split_kernel<KB, VB, QJL, GC, OD, X1>,
                                                          Cfg<VB, GC, QJL, (OD > 0)>::NT, 0) != hipSuccess ||
             o < 1)
             o = 1;
@@ -1538,10 +1613,10 @@ int choose_split(int groups, int64_t n_tokens, int target_wgs, int nw, int64_t* 
     return (int)(got > 0 ? got : 1);
 }
 
-template <int KB, int VB, bool QJL, int GC, int OD = 0>
+template <int KB, int VB, bool QJL, int GC, int OD = 0, int X1 = 0>
 int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out, int64_t* tps_out) {
     constexpr bool SPL = OD > 0;
-    const int target = wgs_per_cu<KB, VB, QJL, GC, OD>() * cu_count();
+    const int target = wgs_per_cu<KB, VB, QJL, GC, OD, X1>() * cu_count();
     int64_t tps;
     const int ns = choose_split(groups, a.n_tokens > 0 ? a.n_tokens : 1, target, Cfg<VB, GC, QJL, SPL>::NW, &tps);
     *n_split_out = ns;
@@ -1550,18 +1625,23 @@ int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out
     // descriptors and its token offsets fit 32-bit scalars
     if (tps >= ((int64_t)1 << 24)) return TQ_ERR_UNSUPPORTED;
     if (a.po == nullptr) return TQ_OK;  // sizing query only
-    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC, OD>), dim3(ns, groups), dim3(Cfg<VB, GC, QJL, SPL>::NT), 0, s,
+    hipLaunchKernelGGL((split_kernel<KB, VB, QJL, GC, OD, X1>), dim3(ns, groups), dim3(Cfg<VB, GC, QJL, SPL>::NT), 0, s,
                        a.q, a.q_heads, a.kv_heads, a.G, a.seq_starts, a.seq_lens, a.n_tokens, a.cap, a.kc, a.kn, a.ks,
                        a.kr, a.vc, a.vn, a.Rk, a.S, a.c_mse, a.c_qjl, a.Ck, a.Cv, a.scale, tps, ns, a.po, a.pml, a.og);
     return TQ_OK;
 }
 
 // Two-group layers on the split kernel (at most 4 heads per KV head; group 1 at most OD1
-// channels): group 0's bit widths as for a one-group layer, OD = 4 or 8 per-lane dims.
+// channels): group 0's bit widths as for a one-group layer, OD = 4 or 8 per-lane dims, group
+// 1's widths one bit wider (the reference's default) as constants or any widths at run time.
 template <int KB, int VB, bool QJL>
 int launch_split_og(const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
-    if (a.og.d1 <= 4) return launch_split<KB, VB, QJL, 1, 4>(a, groups, s, ns, tps);
-    return launch_split<KB, VB, QJL, 1, OD1>(a, groups, s, ns, tps);
+    const bool x1 = a.og.b1k == KB + 1 && a.og.b1v == VB + 1;
+    if (a.og.d1 <= 4)
+        return x1 ? launch_split<KB, VB, QJL, 1, 4, 1>(a, groups, s, ns, tps)
+                  : launch_split<KB, VB, QJL, 1, 4, 0>(a, groups, s, ns, tps);
+    return x1 ? launch_split<KB, VB, QJL, 1, OD1, 1>(a, groups, s, ns, tps)
+              : launch_split<KB, VB, QJL, 1, OD1, 0>(a, groups, s, ns, tps);
 }
 
 int dispatch_og(int value_bits, int has_qjl, const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
