@@ -497,6 +497,28 @@ def test_split_full_size_c2_layer_attention(cuda):
         assert err <= TOL, (b, err)
 
 
+@pytest.mark.parametrize("bits,qjl", [(4, True), (3, False)])
+def test_split_layer_diffuse_softmax_long_context(cuda, bits, qjl):
+    """An evenly spread softmax over 131,072 tokens (queries scaled by 1e-3) on the
+    matrix-core path of a split layer: the normal group's fp16 value sums take the balanced
+    codebook at its own dimension (124 channels), which keeps the near-cancelling average
+    within 2e-3 of the fp64 formula."""
+    B, Hq, Hkv, N = 1, 8, 2, 131072
+    kx = kv_bf16((B, Hkv, N, D), seed=90 + bits, device=cuda, outlier_channels=4)
+    vx = kv_bf16((B, Hkv, N, D), seed=91 + bits, device=cuda)
+    layer = PackedMSELayer(bits=bits, num_outlier_channels=4, use_qjl_keys=qjl, quantize_decode=True)
+    layer.initialize_from_dense(kx, vx)
+    del kx, vx
+    sc = layer._split
+    q = (query_bf16(B, Hq, D, seed=92, device=cuda).float() * 1e-3).to(torch.bfloat16)
+    _, out = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=N, key_stack=sc.key_stack,
+                                       value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, want_f32=True)
+    ref = O.split_fused_attention_f64(u16(q), _host_groups(layer), D)
+    err = np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max()
+    print(f"[split-diffuse] bits {bits} qjl {qjl}: {err:.2e} of |out|_inf", flush=True)
+    assert err <= TOL, err
+
+
 @pytest.mark.parametrize("bits,qjl", [(5, False), (8, False), (6, True)])
 def test_single_group_attention_at_wide_bit_widths(cuda, bits, qjl):
     """One group of all 128 channels (n_groups = 1): the unsplit layer at widths the MFMA
