@@ -184,8 +184,9 @@ def bench_split(args, dev) -> dict:
     avg_us = e0.elapsed_time(e1) * 1e3 / (args.steps * args.layers)
     layer_bytes = int(layers[0].storage_bytes())
     achieved = layer_bytes / (avg_us * 1e-6) / 1e9
-    # at most 4 heads per KV head and 8 outlier channels: the split kernel's matrix-core path
-    mfma = Hq // Hkv <= 4 and args.outliers <= 8
+    # at most 8 outlier channels, and with 5-8 heads per KV head not 3-bit Q_mse (the outlier
+    # group here is one bit wider): the split kernel's matrix-core path
+    mfma = args.outliers <= 8 and (Hq // Hkv <= 4 or qjl or bits != 3)
     return {
         "metric": "outlier-split decode-attn us/layer, 8B KV shape @32K",
         "value": round(avg_us, 1),

@@ -441,12 +441,17 @@ def _rows_range(groups: list[dict], b: int, start: int, end: int) -> list[dict]:
     (3, False, 7, 1, 8, 2),
     (2, False, 3, 2, 4, 1),
     (1, False, 6, 3, 12, 3),
+    (4, True, 4, 1, 28, 4),   # 5-8 heads per KV head (one bit wider outlier group): GQA 7
+    (4, True, 8, 1, 40, 8),   # GQA 5, 8 outlier channels
+    (3, True, 3, 1, 16, 2),   # GQA 8, 3-bit Q_prod
+    (2, False, 5, 1, 24, 4),  # GQA 6, 2-bit Q_mse
+    (4, False, 4, 1, 12, 2),  # GQA 6, 4-bit Q_mse
 ])
 def test_split_layer_matrix_core_attention(cuda, bits, qjl, k, extra, Hq, Hkv):
-    """Two-group layers with at most 4 query heads per KV head and at most 8 outlier
-    channels run on the matrix-core split kernel (group 0's rows at any byte alignment,
-    group 1 per lane): fp32 output against the fp64 formula over the groups at 2e-3, over
-    the whole range and over per-row ranges (a 1-token row, an offset start)."""
+    """Two-group layers with at most 8 outlier channels (and, at 5-8 query heads per KV head,
+    an outlier group one bit wider) run on the matrix-core split kernel (group 0's rows at any
+    byte alignment, group 1 per lane): fp32 output against the fp64 formula over the groups
+    at 2e-3, over the whole range and over per-row ranges (a 1-token row, an offset start)."""
     B, N = 3, 1237
     kx = kv_bf16((B, Hkv, N, D), seed=70 + k, device=cuda, outlier_channels=k)
     vx = kv_bf16((B, Hkv, N, D), seed=71 + k, device=cuda)
@@ -494,6 +499,29 @@ def test_split_full_size_c2_layer_attention(cuda):
         ref = O.split_fused_attention_f64(u16(q)[b:b + 1], _rows_range(host, b, 0, N), D)[0]
         err = np.abs(of[b] - ref).max() / np.abs(ref).max()
         print(f"[split-mfma] C2 split layer, row {b}: {err:.2e}", flush=True)
+        assert err <= TOL, (b, err)
+
+
+def test_split_full_size_c4_layer_attention(cuda):
+    """The config 4 shape (B=4, Hq=28, Hkv=4, N=32768, 4-bit Q_prod, GQA 7) split 124 + 4
+    channels, on the 5-8-head matrix-core split kernel: batch rows 0 and 3 against the fp64
+    formula over the groups at 2e-3."""
+    B, Hq, Hkv, N = 4, 28, 4, 32768
+    kx = kv_bf16((B, Hkv, N, D), seed=2036, device=cuda, outlier_channels=4)
+    vx = kv_bf16((B, Hkv, N, D), seed=2037, device=cuda)
+    layer = PackedMSELayer(bits=4, num_outlier_channels=4, use_qjl_keys=True, quantize_decode=True)
+    layer.initialize_from_dense(kx, vx)
+    del kx, vx
+    sc = layer._split
+    q = query_bf16(B, Hq, D, seed=2038, device=cuda)
+    _, of = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=N, key_stack=sc.key_stack,
+                                      value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, want_f32=True)
+    of = of.cpu().numpy()
+    host = _host_groups(layer)
+    for b in (0, 3):
+        ref = O.split_fused_attention_f64(u16(q)[b:b + 1], _rows_range(host, b, 0, N), D)[0]
+        err = np.abs(of[b] - ref).max() / np.abs(ref).max()
+        print(f"[split-mfma] C4 split layer, row {b}: {err:.2e}", flush=True)
         assert err <= TOL, (b, err)
 
 

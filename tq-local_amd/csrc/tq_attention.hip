@@ -80,13 +80,17 @@ constexpr int D = TQ_DIM;
 #define TQ_ATTN_SETS_G8 2
 #endif
 // layers quantized in two channel groups (SPL): the outlier group's registers take the
-// kernel past 128 VGPRs
+// kernel past 128 VGPRs with up to 4 heads per KV head, past 168 with 5-8
 #ifndef TQ_ATTN_WAVES_SPL
 #define TQ_ATTN_WAVES_SPL 12
 #endif
+#ifndef TQ_ATTN_WAVES_SPL8
+#define TQ_ATTN_WAVES_SPL8 8
+#endif
 template <int VB, int GC, bool QJL, bool SPL = false>
 struct Cfg {
-    static constexpr int NW = SPL ? TQ_ATTN_WAVES_SPL : (GC == 1 ? TQ_ATTN_WAVES_G4 : TQ_ATTN_WAVES_G8);
+    static constexpr int NW = SPL ? (GC == 1 ? TQ_ATTN_WAVES_SPL : TQ_ATTN_WAVES_SPL8)
+                                  : (GC == 1 ? TQ_ATTN_WAVES_G4 : TQ_ATTN_WAVES_G8);
     static constexpr int NT = NW * 64;
     // per-wave blocks in flight (register sets of packed data)
     static constexpr int NSET = GC == 1 ? TQ_ATTN_SETS_G4 : TQ_ATTN_SETS_G8;
@@ -255,12 +259,13 @@ constexpr int WROW = 16;  // dwords per row of the weight transpose: 4 lane grou
 template <int KB, int VB>
 constexpr int PAIR_ENTRIES = (1 << (2 * KB)) > (1 << (2 * VB)) ? (1 << (2 * KB)) : (1 << (2 * VB));
 
-// LDS scratch of the image builder
-template <int GC>
+// LDS scratch of the image builder (QR: q R_k^T kept, for the int8 key image or the outlier
+// group of a two-group layer)
+template <int GC, bool QR = GC == 1>
 struct PrepLds {
     static constexpr int NH = 4 * GC;
     float qp[NH][D];                  // q S^T of the group's heads
-    float qr[GC == 1 ? NH : 1][D];    // q R_k^T times the logit scale (int8 key image)
+    float qr[QR ? NH : 1][D];         // q R_k^T times the logit scale
     float red[16];                    // max |.| per matrix-core tile: R_k tiles 0..7, S tiles 8..15
 };
 
@@ -268,18 +273,18 @@ struct PrepLds {
 // looked up in pair tables of (C[c0], C[c1]) where the widths allow (keys up to 4 bits, values
 // up to 5 bits with OD = 4, 4 with OD = 8), single codes in the codebooks otherwise.
 constexpr int OD1 = 8;
-template <int OD>
+template <int OD, int NH>
 struct OutLds {
     static constexpr int KP = 256, VP = OD == 4 ? 1024 : 256;  // pair-table entries
-    float q1[4][OD];        // per query head: q_rot of the group's dims (log2 units)
-    float ts[4][1 << OD];   // per query head: sum of q_proj (times the QJL scale) over the dims whose sign bit is set
+    float q1[NH][OD];       // per query head: q_rot of the group's dims (log2 units)
+    float ts[NH][1 << OD];  // per query head: sum of q_proj (times the QJL scale) over the dims whose sign bit is set
     float ck[256];          // the group's key and value codebooks (up to 8 bits)
     float cv[256];
     float2 tk[KP];          // key code pairs
     float2 tv[VP];          // value code pairs
 };
-template <>
-struct OutLds<0> {};
+template <int NH>
+struct OutLds<0, NH> {};
 
 template <int KB, int VB, bool QJL, int GC, int OD = 0>
 struct Smem {
@@ -305,7 +310,7 @@ struct Smem {
         struct {
             uint4 img[IMG_DW / 4];      // this group's q-side image
             uint4 qst[NW][NH * 16 > 128 ? NH * 16 : 128];  // per wave: the query rows, then the R_k / S restage
-            PrepLds<GC> ps;             // scratch of the image builder
+            PrepLds<GC, (GC == 1 || SPL)> ps;  // scratch of the image builder
         } pro;
         struct {
             float o[NW][NH][D];
@@ -314,7 +319,7 @@ struct Smem {
         } epi;
     } u;
     uint32_t wt[NW][Cfg<VB, GC, QJL, SPL>::NB][16][WROW];   // per-wave transposes of the softmax weights
-    OutLds<OD> ol;
+    OutLds<OD, NH> ol;
 };
 
 // LDS byte offset (from T0's base) of the table entry of the 6-bit field at bit p of the word
@@ -475,11 +480,11 @@ __device__ __forceinline__ void split3_bf16(const f32x4& a, const f32x4& b, u32x
 // operand loads are issued and before they are waited for: global loads complete in issue
 // order, so loads that mid() issues stay in flight through the products (and the barriers,
 // which wait for LDS only).
-template <bool QJL, int GC, int NW, bool KI8, typename Mid>
+template <bool QJL, int GC, int NW, bool KI8, bool QR, typename Mid>
 __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, int G, int bh0,
                                                const float* __restrict__ Rk, const float* __restrict__ S,
-                                               float c_mse, PrepLds<GC>& L, uint32_t* img, uint4* qst,
-                                               int wave, int lane, Mid&& mid) {
+                                               float c_mse, PrepLds<GC, QR>& L, uint32_t* img, uint4* qst,
+                                               int wave, int lane, int d0, Mid&& mid) {
     using R = Rows<GC>;
     constexpr int NH = R::NH;
     constexpr int NTILE = QJL ? 16 : 8;
@@ -558,10 +563,14 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int h = 4 * kq + i;
-                    const float x = acc[i] * c_mse;  // scores come out in log2 units
+                    // scores come out in log2 units; dims >= d0 (a two-group layer's outlier
+                    // group) are zero here and kept in L.qr for their own term
+                    const float xr = acc[i] * c_mse;
+                    const float x = j < d0 ? xr : 0.0f;
                     const float xh = bf16_val(bf16_bits(x));
                     base[R::row(h, 0) * 4] = dup_bf16(xh);
                     base[R::row(h, 1) * 4] = dup_bf16(x - xh);
+                    if constexpr (QR) L.qr[h][j] = xr;
                 }
             }
         } else {
@@ -593,8 +602,8 @@ __device__ __forceinline__ void image_products(const uint16_t* __restrict__ q, i
 // Phase 2 (after a barrier): the QJL fixed-point exponent G2 (max |q_proj| 2^(G2 - 7) < 2^22,
 // G2 - 7 capped at 60) and the limb image of dims d < d0 (zero beyond: the outlier group of a
 // two-group layer has its own term).  Returns G2 in every thread.
-template <int GC, int NT>
-__device__ __forceinline__ int qjl_image(const PrepLds<GC>& L, uint32_t* img, int tid, int d0) {
+template <int GC, int NT, bool QR>
+__device__ __forceinline__ int qjl_image(const PrepLds<GC, QR>& L, uint32_t* img, int tid, int d0) {
     constexpr int NH = 4 * GC;
     float mx = 0.0f;
 #pragma unroll
@@ -708,7 +717,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     const float* __restrict__ Ck, const float* __restrict__ Cv, float scale,
     int64_t tokens_per_split, int n_split, float* __restrict__ part_o, float* __restrict__ part_ml, Og og) {
     constexpr bool SPL = OD > 0;
-    static_assert(!SPL || (GC == 1 && OD <= OD1), "two-group layers: at most 4 heads per KV head, OD <= OD1");
+    static_assert(!SPL || OD <= OD1, "two-group layers: at most OD1 outlier dims per lane");
     using Sm = Smem<KB, VB, QJL, GC, OD>;
     using R = Rows<GC>;
     constexpr bool KI8 = Sm::KI8;
@@ -960,7 +969,8 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
         E = 15 - e;
     }
     constexpr int PRO_SETS = Cfg<VB, GC, QJL, SPL>::PRO_SETS;
-    image_products<QJL, GC, NW, KI8>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, sm.u.pro.qst[wave], wave, lane, [&] {
+    image_products<QJL, GC, NW, KI8, (GC == 1 || SPL)>(q, G, bh0, Rk, S, c_mse, sm.u.pro.ps, img, sm.u.pro.qst[wave], wave,
+                                                       lane, SPL ? og.d0 : D, [&] {
         ck_e = Ck[tid & ((1 << KB) - 1)];
         cv_e = Cv[tid & ((1 << VB) - 1)];
         if constexpr (SPL) {
@@ -1046,11 +1056,12 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
         // sum of q_proj times the QJL scale over the dims whose bit is set in s, in ascending
         // order) and the code-pair tables (pair index = c0 + c1 2^b, as the two codes lie in
         // the row)
-        if (tid < 4 * OD) {
+        constexpr int NH = R::NH;
+        if (tid < NH * OD) {
             const int h = tid / OD, j = tid % OD;
             sm.ol.q1[h][j] = j < og.d1 ? sm.u.pro.ps.qr[h][d0 + j] : 0.0f;
         }
-        for (int i = tid; i < (4 << OD); i += NT) {
+        for (int i = tid; i < (NH << OD); i += NT) {
             const int h = i >> OD, sg = i & ((1 << OD) - 1);
             float t = 0.0f;
             for (int j = 0; j < og.d1; ++j)
@@ -1064,7 +1075,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
             for (int i = tid; i < (1 << (2 * b1v)); i += NT)
                 sm.ol.tv[i] = make_float2(sm.ol.cv[i & ((1 << b1v) - 1)], sm.ol.cv[i >> b1v]);
     }
-    if constexpr (QJL || KI8) __syncthreads();
+    if constexpr (QJL || KI8 || SPL) __syncthreads();
     // phase 3: operands into registers.  A operands of the key-score MFMAs: int8 keys, lane
     // (row 4 h + s, g), MFMA j: digits of dims 32 g + 8 j .. + 7 (16 VGPRs); bf16 keys, lane
     // (n, g), MFMA j, VGPR r holds q_x[h][32 g + 4 j + r] twice (32 VGPRs).
@@ -1077,15 +1088,21 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
     // group 1 of a two-group layer, for lane group g's head: q_rot (log2 units) of dims d0 ..
     // d0 + OD - 1, zero past d1, so the codes read there add nothing; the sum of its q_proj
     // (times the QJL scale); the group's value sums o1, rescaled with the MFMA sums
-    float q1r[SPL ? OD : 1], o1[SPL ? OD : 1], sq1 = 0.0f;
+    constexpr int OD_ = SPL ? OD : 1;
+    float q1r[R::HPL][OD_], o1[R::HPL][OD_], sq1[R::HPL];
     const float ikscale = 1.0f / kscale;  // a power of two
-    if constexpr (SPL) {
 #pragma unroll
-        for (int j = 0; j < OD; ++j) {
-            q1r[j] = sm.ol.q1[g][j];
-            o1[j] = 0.0f;
+    for (int i = 0; i < R::HPL; ++i) {
+        sq1[i] = 0.0f;
+        if constexpr (SPL) {
+            const int h = R::HPL * g + i;
+#pragma unroll
+            for (int j = 0; j < OD; ++j) {
+                q1r[i][j] = sm.ol.q1[h][j];
+                o1[i][j] = 0.0f;
+            }
+            sq1[i] = sm.ol.ts[h][(1 << OD) - 1];
         }
-        sq1 = sm.ol.ts[g][(1 << OD) - 1];
     }
     // A operands of the QJL MFMAs: rows = (head, limb); MFMA jj, VGPR v, byte e <-> dim
     // 32 g + 4 jj + v + 8 e.
@@ -1291,28 +1308,41 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
             g1n = half(__builtin_amdgcn_perm(O.kr, O.kn, 0x05040100u));  // |k1| | |r1| << 16
             g1vn = half(O.vn);
         }
-        float l1[NB];
+        float l1[NB][R::HPL];
         if constexpr (SPL) {
             const uint64_t m1k = (1ull << b1k) - 1u;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const uint64_t kb = ((uint64_t)g1k[1] << 32) | g1k[0];
-                float a = 0.0f;
+                float a[R::HPL];
+#pragma unroll
+                for (int i = 0; i < R::HPL; ++i) a[i] = 0.0f;
                 if (kpair) {
                     const uint64_t mp = (1ull << (2 * b1k)) - 1u;
 #pragma unroll
                     for (int p = 0; p < OD / 2; ++p) {
                         const float2 e = sm.ol.tk[(uint32_t)((kb >> (2 * p * b1k)) & mp)];
-                        a = __builtin_fmaf(q1r[2 * p], e.x, a);
-                        a = __builtin_fmaf(q1r[2 * p + 1], e.y, a);
+#pragma unroll
+                        for (int i = 0; i < R::HPL; ++i) {
+                            a[i] = __builtin_fmaf(q1r[i][2 * p], e.x, a[i]);
+                            a[i] = __builtin_fmaf(q1r[i][2 * p + 1], e.y, a[i]);
+                        }
                     }
                 } else {
 #pragma unroll
-                    for (int j = 0; j < OD; ++j) a = __builtin_fmaf(q1r[j], sm.ol.ck[(uint32_t)((kb >> (j * b1k)) & m1k)], a);
+                    for (int j = 0; j < OD; ++j) {
+                        const float c = sm.ol.ck[(uint32_t)((kb >> (j * b1k)) & m1k)];
+#pragma unroll
+                        for (int i = 0; i < R::HPL; ++i) a[i] = __builtin_fmaf(q1r[i][j], c, a[i]);
+                    }
                 }
-                const float qs = QJL ? sm.ol.ts[g][g1s & ((1u << OD) - 1u)] : 0.0f;
-                const float v = tq::f16_to_f32(g1n & 0xFFFFu) * a;
-                l1[b] = QJL ? __builtin_fmaf(tq::f16_to_f32(g1n >> 16), __builtin_fmaf(2.0f, qs, -sq1), v) : v;
+                const float kn1 = tq::f16_to_f32(g1n & 0xFFFFu), kr1 = tq::f16_to_f32(g1n >> 16);
+#pragma unroll
+                for (int i = 0; i < R::HPL; ++i) {
+                    const float qs = QJL ? sm.ol.ts[R::HPL * g + i][g1s & ((1u << OD) - 1u)] : 0.0f;
+                    const float v = kn1 * a[i];
+                    l1[b][i] = QJL ? __builtin_fmaf(kr1, __builtin_fmaf(2.0f, qs, -sq1[i]), v) : v;
+                }
             }
         }
         // ---- scores
@@ -1345,7 +1375,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
                 } else {
                     v = knf * ksum;
                 }
-                if constexpr (SPL) v = __builtin_fmaf(l1[b], ikscale, v);
+                if constexpr (SPL) v = __builtin_fmaf(l1[b][i], ikscale, v);
                 lg[b][i] = valid ? v : NEG_INF;
                 over |= __builtin_fmaf(lg[b][i], kscale, ev[b]) > m_thr[i];
             }
@@ -1374,7 +1404,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
                 }
                 if constexpr (SPL) {
 #pragma unroll
-                    for (int j = 0; j < OD; ++j) o1[j] *= a;
+                    for (int j = 0; j < OD; ++j) o1[i][j] *= a;
                 }
                 m_ref[i] = mn;
                 m_thr[i] = mn + (WEXP0 + LAZY_MAX);
@@ -1382,7 +1412,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
         }
         // ---- weights
         u32x4 av[NB];
-        float pv1[NB];  // group 1: p |v1| of token n (head g)
+        float pv1[NB][R::HPL];  // group 1: p |v1| of token n, the lane's heads
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             uint32_t(*wt)[WROW] = sm.wt[wave][b];
@@ -1390,7 +1420,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
 #pragma unroll
             for (int i = 0; i < R::HPL; ++i) {
                 const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(lg[b][i], kscale, -m_ref[i]));
-                if constexpr (SPL) pv1[b] = p * tq::f16_to_f32(g1vn);
+                if constexpr (SPL) pv1[b][i] = p * tq::f16_to_f32(g1vn);
                 s_lane[i] += p;
                 const uint16_t w = (uint16_t)tq::f32_to_f16(__builtin_fmaf(vnf, p, 0.0f));
                 const int h = R::HPL * g + i;
@@ -1452,13 +1482,19 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
 #pragma unroll
                     for (int p = 0; p < OD / 2; ++p) {
                         const float2 e = sm.ol.tv[(uint32_t)((vb >> (2 * p * b1v)) & mp)];
-                        o1[2 * p] = __builtin_fmaf(pv1[b], e.x, o1[2 * p]);
-                        o1[2 * p + 1] = __builtin_fmaf(pv1[b], e.y, o1[2 * p + 1]);
+#pragma unroll
+                        for (int i = 0; i < R::HPL; ++i) {
+                            o1[i][2 * p] = __builtin_fmaf(pv1[b][i], e.x, o1[i][2 * p]);
+                            o1[i][2 * p + 1] = __builtin_fmaf(pv1[b][i], e.y, o1[i][2 * p + 1]);
+                        }
                     }
                 } else {
 #pragma unroll
-                    for (int j = 0; j < OD; ++j)
-                        o1[j] = __builtin_fmaf(pv1[b], sm.ol.cv[(uint32_t)((vb >> (j * b1v)) & m1v)], o1[j]);
+                    for (int j = 0; j < OD; ++j) {
+                        const float c = sm.ol.cv[(uint32_t)((vb >> (j * b1v)) & m1v)];
+#pragma unroll
+                        for (int i = 0; i < R::HPL; ++i) o1[i][j] = __builtin_fmaf(pv1[b][i], c, o1[i][j]);
+                    }
                 }
             }
         }
@@ -1519,7 +1555,7 @@ __global__ __launch_bounds__((Cfg<VB, GC, QJL, (OD > 0)>::NT)) void split_kernel
             // read past group 0's rows); the wave's LDS writes execute in program order
 #pragma unroll
             for (int j = 0; j < OD; ++j) {
-                const float t = row_sum16(o1[j]);
+                const float t = row_sum16(o1[i][j]);
                 if (n == 0 && j < og.d1) sm.u.epi.o[wave][h][og.d0 + j] = t;
             }
         }
@@ -1631,32 +1667,47 @@ int launch_split(const SplitArgs& a, int groups, hipStream_t s, int* n_split_out
     return TQ_OK;
 }
 
-// Two-group layers on the split kernel (at most 4 heads per KV head; group 1 at most OD1
-// channels): group 0's bit widths as for a one-group layer, OD = 4 or 8 per-lane dims, group
-// 1's widths one bit wider (the reference's default) as constants or any widths at run time.
+// Two-group layers on the split kernel (group 1 at most OD1 channels): group 0's bit widths as
+// for a one-group layer, OD = 4 or 8 per-lane dims, group 1's widths one bit wider (the
+// reference's default) as constants, or with up to 4 heads per KV head any widths at run time
+// (the host sends 5-8 heads with other widths to the fp32 kernel).
+constexpr bool og_wide_ok(int kb, int vb, bool qjl) { return !(kb == 3 && vb == 3 && !qjl); }
+
 template <int KB, int VB, bool QJL>
-int launch_split_og(const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
+int launch_split_og(int G, const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
     const bool x1 = a.og.b1k == KB + 1 && a.og.b1v == VB + 1;
-    if (a.og.d1 <= 4)
+    const bool od4 = a.og.d1 <= 4;
+    if (G > 4) {
+        // 3-bit Q_mse at 5-8 heads: the byte-window tables leave no LDS for the outlier group
+        if constexpr (og_wide_ok(KB, VB, QJL)) {
+            if (!x1) return TQ_ERR_UNSUPPORTED;
+            return od4 ? launch_split<KB, VB, QJL, 2, 4, 1>(a, groups, s, ns, tps)
+                       : launch_split<KB, VB, QJL, 2, OD1, 1>(a, groups, s, ns, tps);
+        } else {
+            return TQ_ERR_UNSUPPORTED;
+        }
+    }
+    if (od4)
         return x1 ? launch_split<KB, VB, QJL, 1, 4, 1>(a, groups, s, ns, tps)
                   : launch_split<KB, VB, QJL, 1, 4, 0>(a, groups, s, ns, tps);
     return x1 ? launch_split<KB, VB, QJL, 1, OD1, 1>(a, groups, s, ns, tps)
               : launch_split<KB, VB, QJL, 1, OD1, 0>(a, groups, s, ns, tps);
 }
 
-int dispatch_og(int value_bits, int has_qjl, const SplitArgs& a, int groups, hipStream_t s, int* ns, int64_t* tps) {
+int dispatch_og(int value_bits, int has_qjl, int G, const SplitArgs& a, int groups, hipStream_t s, int* ns,
+                int64_t* tps) {
     if (has_qjl) {
         switch (value_bits) {
-            case 2: return launch_split_og<1, 2, true>(a, groups, s, ns, tps);
-            case 3: return launch_split_og<2, 3, true>(a, groups, s, ns, tps);
-            default: return launch_split_og<3, 4, true>(a, groups, s, ns, tps);
+            case 2: return launch_split_og<1, 2, true>(G, a, groups, s, ns, tps);
+            case 3: return launch_split_og<2, 3, true>(G, a, groups, s, ns, tps);
+            default: return launch_split_og<3, 4, true>(G, a, groups, s, ns, tps);
         }
     }
     switch (value_bits) {
-        case 1: return launch_split_og<1, 1, false>(a, groups, s, ns, tps);
-        case 2: return launch_split_og<2, 2, false>(a, groups, s, ns, tps);
-        case 3: return launch_split_og<3, 3, false>(a, groups, s, ns, tps);
-        default: return launch_split_og<4, 4, false>(a, groups, s, ns, tps);
+        case 1: return launch_split_og<1, 1, false>(G, a, groups, s, ns, tps);
+        case 2: return launch_split_og<2, 2, false>(G, a, groups, s, ns, tps);
+        case 3: return launch_split_og<3, 3, false>(G, a, groups, s, ns, tps);
+        default: return launch_split_og<4, 4, false>(G, a, groups, s, ns, tps);
     }
 }
 
@@ -2205,13 +2256,16 @@ extern "C" int tq_decode_attention_groups(const uint16_t* q, int batch, int q_he
     if (dsum != D) return TQ_ERR_INVALID_ARGUMENT;  // the groups partition the head's channels
     const int groups = batch * kv_heads;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // Two groups with at most 4 query heads per KV head and at most OD1 outlier channels: the
-    // split kernel's matrix-core stages for group 0 and a per-lane term for group 1, when group
-    // 0's bit widths are a one-group layer's and the row arrays start at 4-byte boundaries
+    // Two groups with at most OD1 outlier channels: the split kernel's matrix-core stages for
+    // group 0 and a per-lane term for group 1, when group 0's bit widths are a one-group
+    // layer's, group 1 is one bit wider or there are at most 4 query heads per KV head, and the
+    // row arrays start at 4-byte boundaries
     const auto a4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; };
     const bool og_bits = has_qjl ? (key_bits[0] + 1 == value_bits[0] && value_bits[0] >= 2 && value_bits[0] <= 4)
                                  : (key_bits[0] == value_bits[0] && key_bits[0] >= 1 && key_bits[0] <= 4);
-    bool og_ok = n_groups == 2 && G <= 4 && sub_dims[1] <= OD1 && og_bits && aligned16(q);
+    const bool og_x1 = n_groups == 2 && key_bits[1] == key_bits[0] + 1 && value_bits[1] == value_bits[0] + 1;
+    bool og_ok = n_groups == 2 && (G <= 4 || (og_x1 && og_wide_ok(key_bits[0], value_bits[0], has_qjl))) &&
+                 sub_dims[1] <= OD1 && og_bits && aligned16(q);
     for (int g = 0; og_ok && g < 2; ++g)
         og_ok = a4(k_codes[g]) && a4(v_codes[g]) && (!has_qjl || a4(k_signs[g]));
     if (og_ok) {
@@ -2233,14 +2287,14 @@ extern "C" int tq_decode_attention_groups(const uint16_t* q, int batch, int q_he
         o.cq1 = (float)(scale * LOG2E * (qs / d1));
         int n_split = 0;
         int64_t tps = 0;
-        int st = dispatch_og(value_bits[0], has_qjl, sa, groups, s, &n_split, &tps);  // sizing
+        int st = dispatch_og(value_bits[0], has_qjl, G, sa, groups, s, &n_split, &tps);  // sizing
         if (st != TQ_OK) return st;
         const Ws w = ws_layout(batch, q_heads, n_split);
         if (workspace_bytes < w.total) return TQ_ERR_WORKSPACE;
         char* base = static_cast<char*>(workspace);
         sa.po = reinterpret_cast<float*>(base + w.po);
         sa.pml = reinterpret_cast<float*>(base + w.pml);
-        st = dispatch_og(value_bits[0], has_qjl, sa, groups, s, &n_split, &tps);
+        st = dispatch_og(value_bits[0], has_qjl, G, sa, groups, s, &n_split, &tps);
         if (st != TQ_OK) return st;
         TQ_CHECK_LAUNCH();
         hipLaunchKernelGGL(merge_kernel, dim3(batch * q_heads), dim3(MT), 0, s, sa.po, sa.pml, n_split, value_matrix,
