@@ -246,11 +246,12 @@ int tq_dequantize_group(const uint8_t* codes, const uint16_t* norms, const uint8
  * sub_dims, key_bits and value_bits are host arrays too.  key_centers[g] /
  * value_centers[g] are the groups' codebooks.
  *
- * Two groups with at most 4 query heads per KV head, at most 8 channels in group 1, group
- * 0's bit widths as tq_decode_attention takes them and the code and sign arrays at 4-byte
- * boundaries run on tq_decode_attention's matrix-core kernel: group 0 there (its value sums
- * in fp16, so value_centers[0] is best given as tq_value_codebook_f16(..., sub_dims[0], ...)),
- * group 1 in fp32 per lane.  Other layers run on an fp32 kernel.
+ * Two groups with at most 8 channels in group 1, group 0's bit widths as tq_decode_attention
+ * takes them, the code and sign arrays at 4-byte boundaries, and either at most 4 query heads
+ * per KV head or group 1 one bit wider than group 0 (not with 3-bit Q_mse group 0) run on
+ * tq_decode_attention's matrix-core kernel: group 0 there (its value sums in fp16, so
+ * value_centers[0] is best given as tq_value_codebook_f16(..., sub_dims[0], ...)), group 1 in
+ * fp32 per lane.  Other layers run on an fp32 kernel.
  *
  * key_matrix, qjl_matrix, value_matrix: [dim][dim] device matrices (16-byte aligned)
  * stacking the groups' channel-space matrices (tq_group_matrix), group 0's sub_dims[0]
