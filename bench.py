@@ -234,7 +234,8 @@ def bench_c5(args, dev) -> dict:
     """a random-init QwQ-32B-architecture model (Qwen2, 64 layers, hidden
     5120, 40/8 heads, SwiGLU 27648, vocab 152064, rope theta 1e6, bf16) on one GPU; 131072
     uniform random prompt ids, then 512 greedy tokens with EOS disabled, through
-    turboquant.activate(bits=4, Q_prod keys, quantize_decode=True) and model.generate."""
+    turboquant.activate(bits=4, Q_prod keys, quantize_decode=True) and model.generate;
+    with --outliers K every packed layer is split (num_outlier_channels=K)."""
     import torch
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
@@ -262,7 +263,8 @@ def bench_c5(args, dev) -> dict:
     init_s = time.perf_counter() - t0
     print(f"[bench] c5 model ready in {init_s:.1f} s ({sum(p.numel() for p in model.parameters()) / 1e9:.2f} B "
           "parameters)", file=sys.stderr, flush=True)
-    turboquant.activate(model, _IdTokenizer(), bits=4, use_qjl_keys=True, quantize_decode=True, quiet=True)
+    turboquant.activate(model, _IdTokenizer(), bits=4, use_qjl_keys=True, quantize_decode=True, quiet=True,
+                        num_outlier_channels=args.outliers)
     ids = torch.randint(0, cfg.vocab_size, (1, prompt), generator=torch.Generator().manual_seed(5)).to(dev)
     model.generate(ids[:, :2048], max_new_tokens=4)  # untimed: kernel loading, GEMM heuristics, allocator
     runs = {}
@@ -282,23 +284,39 @@ def bench_c5(args, dev) -> dict:
     torch.cuda.empty_cache()
     # the decode attention kernel alone on one packed layer of the final shape (N = prompt + new)
     N = prompt + new
-    lc = layer_codecs(128, 4, 0, True, dev)
     k, v = kv_bf16((1, 8, N, 128), seed=1, device=dev), kv_bf16((1, 8, N, 128), seed=2, device=dev)
-    L = {"k_codes": torch.empty(1, 8, N, 48, dtype=torch.uint8, device=dev),
-         "k_norms": torch.empty(1, 8, N, dtype=torch.float16, device=dev),
-         "k_signs": torch.empty(1, 8, N, 16, dtype=torch.uint8, device=dev),
-         "k_rnorms": torch.empty(1, 8, N, dtype=torch.float16, device=dev),
-         "v_codes": torch.empty(1, 8, N, 64, dtype=torch.uint8, device=dev),
-         "v_norms": torch.empty(1, 8, N, dtype=torch.float16, device=dev)}
-    K.quantize_prod(k, lc.key, lc.qjl, L["k_codes"], L["k_norms"], L["k_signs"], L["k_rnorms"])
-    K.quantize_mse(v, lc.value, L["v_codes"], L["v_norms"])
     q = query_bf16(1, 40, 128, seed=3, device=dev)
+    if args.outliers:
+        from turboquant.runtime.attention import _group_buffers
+        from turboquant.runtime.packed_qmse_cache import PackedMSELayer
+
+        layer = PackedMSELayer(bits=4, num_outlier_channels=args.outliers, use_qjl_keys=True, quantize_decode=True,
+                               reserve_tokens=0)
+        layer.initialize_from_dense(k, v)
+        sc, gb = layer._split, _group_buffers(layer)
+
+        def call():
+            K.decode_attention_groups(q, gb, n_tokens=N, key_stack=sc.key_stack, value_stack=sc.value_stack,
+                                      qjl_stack=sc.qjl_stack)
+    else:
+        lc = layer_codecs(128, 4, 0, True, dev)
+        L = {"k_codes": torch.empty(1, 8, N, 48, dtype=torch.uint8, device=dev),
+             "k_norms": torch.empty(1, 8, N, dtype=torch.float16, device=dev),
+             "k_signs": torch.empty(1, 8, N, 16, dtype=torch.uint8, device=dev),
+             "k_rnorms": torch.empty(1, 8, N, dtype=torch.float16, device=dev),
+             "v_codes": torch.empty(1, 8, N, 64, dtype=torch.uint8, device=dev),
+             "v_norms": torch.empty(1, 8, N, dtype=torch.float16, device=dev)}
+        K.quantize_prod(k, lc.key, lc.qjl, L["k_codes"], L["k_norms"], L["k_signs"], L["k_rnorms"])
+        K.quantize_mse(v, lc.value, L["v_codes"], L["v_norms"])
+
+        def call():
+            K.decode_attention(q, n_tokens=N, key=lc.key, value=lc.value, qjl=lc.qjl, **L)
     for _ in range(3):
-        K.decode_attention(q, n_tokens=N, key=lc.key, value=lc.value, qjl=lc.qjl, **L)
+        call()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(20):
-        K.decode_attention(q, n_tokens=N, key=lc.key, value=lc.value, qjl=lc.qjl, **L)
+        call()
     e1.record()
     torch.cuda.synchronize()
     attn_us = e0.elapsed_time(e1) * 1e3 / 20
@@ -312,7 +330,8 @@ def bench_c5(args, dev) -> dict:
         "dtype": "bf16 model; u8 packed KV",
         "data": "synthetic (uniform random ids, random-init weights)",
         "config": {"workload": f"QwQ-32B architecture, {cfg.num_hidden_layers} layers, prompt {prompt}, "
-                               f"{new} greedy tokens, batch 1, 4-bit Q_prod K / 4-bit Q_mse V, quantize_decode",
+                               f"{new} greedy tokens, batch 1, 4-bit Q_prod K / 4-bit Q_mse V, quantize_decode"
+                               + (f", outlier split ({args.outliers} channels)" if args.outliers else ""),
                    "model_init_s": round(init_s, 1)},
         "decode_ms_per_token": round(step_ms, 3),
         "prefill_and_pack_s": round(runs[2], 2),
@@ -590,7 +609,8 @@ def main() -> int:
                     help="after the timed region, run a plain elementwise copy of one layer's packed size "
                          "(reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--outliers", type=int, default=0,
-                    help="measure outlier-split layers with this many outlier channels instead of the C2 line")
+                    help="measure outlier-split layers with this many outlier channels instead of the C2 line "
+                         "(with --c5: split every layer of the end-to-end run)")
     ap.add_argument("--c5", action="store_true",
                     help="BASELINE config 5 end to end (random-init QwQ-32B architecture) instead of the C2 line")
     ap.add_argument("--c5-layers", type=int, default=64)
@@ -626,11 +646,11 @@ def main() -> int:
     if args.dequant:
         print(json.dumps(bench_dequant(args, dev)))
         return 0
-    if args.outliers:
-        print(json.dumps(bench_split(args, dev)))
-        return 0
     if args.c5:
         print(json.dumps(bench_c5(args, dev)))
+        return 0
+    if args.outliers:
+        print(json.dumps(bench_split(args, dev)))
         return 0
     if args.host:
         print(json.dumps(bench_host(args, dev)))
