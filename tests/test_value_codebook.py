@@ -42,7 +42,7 @@ def best_bias(c32: np.ndarray, P: np.ndarray) -> float:
 
 
 @pytest.mark.parametrize("bits", [1, 2, 3, 4])
-@pytest.mark.parametrize("dim", [128, 64, 16])
+@pytest.mark.parametrize("dim", [128, 124, 64, 16])  # 124: a split layer's normal group
 def test_codebook_f16_is_the_least_biased_choice_of_neighbours(bits, dim):
     c32 = build_scalar_codebook(dim, bits).centers.astype(np.float32)
     out = K.value_codebook_f16(c32, bits, dim)
