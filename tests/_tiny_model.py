@@ -24,11 +24,11 @@ class CharTokenizer:
 
 
 def tiny_llama(device="cpu", dtype=torch.float32, layers: int = 2, heads: int = 8, kv_heads: int = 2, seed: int = 0,
-               vocab: int = 94):
+               vocab: int = 94, hidden: int = 256):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     torch.manual_seed(seed)
-    cfg = LlamaConfig(vocab_size=vocab, hidden_size=256, intermediate_size=512, num_hidden_layers=layers,
+    cfg = LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=512, num_hidden_layers=layers,
                       num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=128,
                       max_position_embeddings=4096, rope_theta=10000.0, attn_implementation="sdpa")
     model = LlamaForCausalLM(cfg).to(device=device, dtype=dtype).eval()

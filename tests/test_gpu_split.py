@@ -396,6 +396,54 @@ def test_activate_generate_with_outlier_split(cuda):
     turboquant.deactivate(model, quiet=True)
 
 
+def test_activate_generate_gqa7_outlier_split_against_oracle(cuda):
+    """activate(num_outlier_channels=4) on a GQA-7 model (14 query heads, 2 KV heads): every
+    layer's decode attention runs on the 5-8-head split kernel; at the last decode step each
+    layer's attention output (captured before o_proj) is the RNE rounding of the kernel's fp32
+    output for the same RoPE'd query, which lies within 2e-3 of the fp64 formula over the groups."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    HQ, HKV, P, NEW = 14, 2, 300, 4
+    model = tiny_llama(device=cuda, dtype=torch.bfloat16, heads=HQ, kv_heads=HKV, hidden=224)
+    turboquant.activate(model, CharTokenizer(), bits=4, num_outlier_channels=4, use_qjl_keys=True,
+                        quantize_decode=True, quiet=True)
+    seen = [{} for _ in model.model.layers]
+    hooks = []
+    for li, dec in enumerate(model.model.layers):
+        att = dec.self_attn
+
+        def pre(mod, args, kwargs, li=li):
+            if getattr(mod, "_tq_cache_layer", None) is not None:
+                seen[li]["layer"] = mod._tq_cache_layer
+
+        hooks.append(att.register_forward_pre_hook(pre, with_kwargs=True))
+        hooks.append(att.q_proj.register_forward_hook(
+            lambda m, a, o, li=li: seen[li].__setitem__("q", o.detach().clone()) if o.shape[1] == 1 else None))
+        hooks.append(att.o_proj.register_forward_pre_hook(
+            lambda m, a, li=li: seen[li].__setitem__("o", a[0].detach().clone()) if a[0].shape[1] == 1 else None))
+    ids = torch.randint(0, 94, (1, P), generator=torch.Generator().manual_seed(3)).to(cuda)
+    out = model.generate(ids, max_new_tokens=NEW)
+    torch.cuda.synchronize()
+    for h in hooks:
+        h.remove()
+    assert out.shape == (1, P + NEW) and torch.equal(out[0, :P], ids[0])
+    pos = P + NEW - 2  # the last decode step fed token NEW - 1 at this position
+    for li, rec in enumerate(seen):
+        layer = rec["layer"]
+        assert layer._split is not None and layer.packed_seq_length() == P + NEW - 1
+        qr = rec["q"].view(1, 1, HQ, D).transpose(1, 2)
+        cos, sin = model.model.rotary_emb(qr, torch.tensor([[pos]], device=cuda))
+        q16, _ = apply_rotary_pos_emb(qr, qr, cos, sin)
+        q16 = q16.to(torch.bfloat16)
+        got32 = fused_attention(q16.float(), layer, HQ // HKV)[:, :, 0]
+        assert np.array_equal(u16(rec["o"].view(1, HQ, D)), O.f32_to_bf16_bits(got32.cpu().numpy())), li
+        ref = O.split_fused_attention_f64(u16(q16[:, :, 0]), _host_groups(layer), D)
+        err = np.abs(got32.cpu().numpy() - ref).max() / np.abs(ref).max()
+        print(f"[split-gqa7] layer {li}: {err:.2e} of |out|_inf", flush=True)
+        assert err <= TOL, (li, err)
+    turboquant.deactivate(model, quiet=True)
+
+
 @pytest.mark.parametrize("Hq,Hkv,bits,extra,k,qjl", [
     (28, 4, 4, 1, 3, True),    # GQA 7 (heads 7 of 8 in the wide kernel)
     (8, 8, 2, 3, 13, True),    # one query head per KV head
