@@ -526,6 +526,31 @@ def test_split_layer_matrix_core_attention(cuda, bits, qjl, k, extra, Hq, Hkv):
         assert err <= TOL, (b, err)
 
 
+@pytest.mark.parametrize("Hq", [8, 14])
+def test_split_layer_empty_ranges_are_zero(cuda, Hq):
+    """The matrix-core split path (GQA 4 and 7) with nothing to attend to: an empty cache
+    (n_tokens = 0) gives zeros and a -inf log-sum-exp, and so does a batch row whose range is
+    empty while the other row is held to the fp64 formula."""
+    B, Hkv, N = 2, 2, 257
+    kx = kv_bf16((B, Hkv, N, D), seed=81, device=cuda, outlier_channels=4)
+    vx = kv_bf16((B, Hkv, N, D), seed=82, device=cuda)
+    layer = PackedMSELayer(bits=4, num_outlier_channels=4, use_qjl_keys=True, quantize_decode=True)
+    layer.initialize_from_dense(kx, vx)
+    sc = layer._split
+    q = query_bf16(B, Hq, D, seed=83, device=cuda)
+    kw = dict(key_stack=sc.key_stack, value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, want_f32=True,
+              want_lse=True)
+    _, out, lse = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=0, **kw)
+    assert float(out.abs().max()) == 0.0 and bool(torch.isneginf(lse).all())
+    starts, ends = torch.tensor([0, 100], dtype=torch.int32), torch.tensor([N, 100], dtype=torch.int32)
+    _, out, lse = K.decode_attention_groups(q, _group_buffers(layer), n_tokens=N, seq_starts=starts, seq_lens=ends,
+                                            **kw)
+    out = out.cpu().numpy()
+    assert np.abs(out[1]).max() == 0.0 and bool(torch.isneginf(lse[1]).all())
+    ref = O.split_fused_attention_f64(u16(q)[:1], _rows_range(_host_groups(layer), 0, 0, N), D)[0]
+    assert np.abs(out[0] - ref).max() <= TOL * np.abs(ref).max()
+
+
 def test_split_full_size_c2_layer_attention(cuda):
     """The headline configuration (B=8, Hq=32, Hkv=8, N=32768, 4-bit Q_prod) split 124 + 4
     channels, at the split kernel's full launch geometry: batch rows 0 and 7 against the fp64
