@@ -551,6 +551,39 @@ def test_split_layer_empty_ranges_are_zero(cuda, Hq):
     assert np.abs(out[0] - ref).max() <= TOL * np.abs(ref).max()
 
 
+def test_split_layer_graph_replay_matches_eager(cuda):
+    """tq_decode_attention_groups on the matrix-core split path (GQA 4 and GQA 7 layers)
+    captured in a HIP graph: bit-identical output on every replay, with eager calls between
+    the replays."""
+    cases = []
+    for Hq, Hkv, N, seed in ((8, 2, 777, 91), (14, 2, 1500, 92)):
+        kx = kv_bf16((2, Hkv, N, D), seed=seed, device=cuda, outlier_channels=4)
+        vx = kv_bf16((2, Hkv, N, D), seed=seed + 1, device=cuda)
+        layer = PackedMSELayer(bits=4, num_outlier_channels=4, use_qjl_keys=True, quantize_decode=True)
+        layer.initialize_from_dense(kx, vx)
+        cases.append((layer, query_bf16(2, Hq, D, seed=seed + 2, device=cuda), N))
+
+    def call(layer, q, n):
+        sc = layer._split
+        return K.decode_attention_groups(q, _group_buffers(layer), n_tokens=n, key_stack=sc.key_stack,
+                                         value_stack=sc.value_stack, qjl_stack=sc.qjl_stack, want_f32=True)[1]
+
+    eager = [call(*c).clone() for c in cases]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [call(*c) for c in cases]
+    for _ in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
+        call(*cases[0])  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_split_full_size_c2_layer_attention(cuda):
     """The headline configuration (B=8, Hq=32, Hkv=8, N=32768, 4-bit Q_prod) split 124 + 4
     channels, at the split kernel's full launch geometry: batch rows 0 and 7 against the fp64
